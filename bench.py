@@ -1,0 +1,266 @@
+"""Benchmark of the causal GQA FlashAttention-2 forward + backward on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--dtype bf16|fp16] [--batch 8] [--seq 1024]
+
+A step is one call pair through the torch.library boundary, ``nanonemo::flash_attn`` then
+``nanonemo::flash_attn_bwd`` (what autograd runs per attention layer), on synthetic N(0,1) inputs
+already resident in HBM. Default workload: B=8, T=1024, 12 query / 4 KV heads, head_dim 64, bf16 (the
+north-star shape of BASELINE.json). The step is captured once into a HIP graph (as the reference's
+benchmark does, /root/reference/benchmarks/kernels/common.py:30-54) and K replays are timed between
+device synchronisations; the eager (uncaptured) time per step is reported beside it.
+
+value = algorithmic FLOPs per step / time per step, with F_alg = 6*B*H*D*T*(T+1) (12*D flop per causal
+(query, key) pair: 2 forward and 4 backward products; the backward's recompute of S is not counted).
+
+The JSON line also carries:
+  roofline      the dominant kernel (the backward main kernel), timed alone with HIP events on the
+                stream it is launched on: achieved = its algorithmic FLOPs (8*D per causal pair) per
+                launch / its mean launch time, against the dense BF16/FP16 MFMA peak of 2.5 PFLOP/s;
+  cpu_baseline  the reference's plain-PyTorch attention (repeat_interleave + SDPA math, forward +
+                autograd) in fp32 on the host cores, on a bounded sample of the same workload;
+  kernels       per-kernel mean times and the preprocessing pass's HBM rate.
+"""
+
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import math
+import os
+import platform
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "causal GQA attn fwd+bwd TFLOP/s at T=1024; % of BF16 MFMA peak"
+PEAK_TFLOPS = 2500.0  # MI355X dense BF16/FP16 MFMA, published
+PEAK_HBM_GBPS = 8000.0
+
+
+def parse():
+    p = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=100)
+    p.add_argument("--warmup", type=int, default=10)
+    p.add_argument("--dtype", choices=["bf16", "fp16"], default="bf16")
+    p.add_argument("--batch", type=int, default=8)
+    p.add_argument("--seq", type=int, default=1024)
+    p.add_argument("--heads", type=int, default=12)
+    p.add_argument("--kv-heads", type=int, default=4)
+    p.add_argument("--head-dim", type=int, default=64)
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--cpu-seconds", type=float, default=10.0, help="budget of the CPU baseline sample")
+    p.add_argument("--profile-only", action="store_true", help="only the timed graph replays (for rocprofv3)")
+    return p.parse_args()
+
+
+def cpu_baseline(B, H, KVH, T, D, budget_s):
+    """Times the reference's plain-PyTorch CPU path (oracle.attention.torch_reference_fwd_bwd) in fp32.
+
+    Sample: one batch element of the workload (B=1, same T, heads and head_dim), repeated for about
+    ``budget_s`` seconds after 3 warm-ups; the median time is scaled to TFLOP/s with the same
+    algorithmic FLOP count as the GPU figure.
+    """
+    import torch
+
+    from oracle.attention import flops, torch_reference_fwd_bwd
+
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    g = torch.Generator().manual_seed(0)
+    q = torch.randn(1, H, T, D, generator=g)
+    k = torch.randn(1, KVH, T, D, generator=g)
+    v = torch.randn(1, KVH, T, D, generator=g)
+    do = torch.randn(1, H, T, D, generator=g)
+    for _ in range(3):
+        torch_reference_fwd_bwd(q, k, v, do)
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while time.perf_counter() < t_end or len(times) < 5:
+        t0 = time.perf_counter()
+        torch_reference_fwd_bwd(q, k, v, do)
+        times.append(time.perf_counter() - t0)
+        if len(times) >= 1000:
+            break
+    t = statistics.median(times)
+    cpu = platform.processor() or platform.machine()
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {
+        "value": flops(1, H, T, D) / t / 1e12,
+        "unit": "TFLOP/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": f"plain-PyTorch causal GQA (repeat_interleave + SDPA math) fwd+autograd bwd, fp32, "
+        f"B=1 of the workload (T={T}, {H}Q/{KVH}KV, d={D}); median of {len(times)} reps "
+        f"({sum(times):.1f} s) = {t * 1e3:.1f} ms",
+        "cpu_model": cpu,
+    }
+
+
+def main():
+    args = parse()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print(
+            "bench.py measures one GPU only: this build's hot path (causal GQA attention) runs per GPU on its "
+            "own heads/batch shard with no exchange, and no multi-GPU figure is produced. Use --gpus 1.",
+            file=sys.stderr,
+        )
+        sys.exit(2)
+
+    import torch
+
+    from nanonemo_amd.kernels.hip import DTYPE_BF16, DTYPE_F16, check, lib
+    from nanonemo_amd.kernels.hip import flash_attn as fa
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    dtype = torch.bfloat16 if args.dtype == "bf16" else torch.float16
+    B, H, KVH, T, D = args.batch, args.heads, args.kv_heads, args.seq, args.head_dim
+    scale = 1.0 / math.sqrt(D)
+    f_fwd = 2.0 * B * H * D * T * (T + 1)
+    f_bwd = 2.0 * f_fwd
+    f_all = f_fwd + f_bwd
+
+    torch.manual_seed(0)
+    q = torch.randn(B, H, T, D, device=dev).to(dtype)
+    k = torch.randn(B, KVH, T, D, device=dev).to(dtype)
+    v = torch.randn(B, KVH, T, D, device=dev).to(dtype)
+    do = torch.randn(B, H, T, D, device=dev).to(dtype)
+
+    def step():
+        o, lse = fa._flash_attn(q, k, v)
+        return fa._flash_attn_bwd(do, q, k, v, o, lse)
+
+    # ---- eager steps (warm-up W, then K timed) ----
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    eager_ms = (time.perf_counter() - t0) * 1e3 / args.steps
+
+    # ---- graph-captured step, K timed replays ----
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(3):
+            step()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    for _ in range(args.warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        graph.replay()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    if args.profile_only:
+        print(json.dumps({"ms_per_step": ms, "eager_ms_per_step": eager_ms}), flush=True)
+        return
+
+    # ---- each kernel alone, HIP events on the launch stream ----
+    L = lib()
+    dt_code = DTYPE_BF16 if dtype == torch.bfloat16 else DTYPE_F16
+    stream = torch.cuda.current_stream()
+    sp = stream.cuda_stream
+    o, lse = fa._flash_attn(q, k, v)
+    ws_bytes = L.nn_fa_bwd_workspace_size(B, H, KVH, T, D)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    launches = {
+        "fwd": lambda: L.nn_fa_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(),
+                                   B, H, KVH, T, D, dt_code, scale, sp),
+        "bwd_pre": lambda: L.nn_fa_bwd_pre(o.data_ptr(), do.data_ptr(), ws.data_ptr(), ws_bytes,
+                                           B, H, KVH, T, D, dt_code, sp),
+        "bwd_main": lambda: L.nn_fa_bwd_main(q.data_ptr(), k.data_ptr(), v.data_ptr(), do.data_ptr(), lse.data_ptr(),
+                                             ws.data_ptr(), ws_bytes, B, H, KVH, T, D, dt_code, scale, sp),
+        "bwd_post": lambda: L.nn_fa_bwd_post(ws.data_ptr(), ws_bytes, dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
+                                             B, H, KVH, T, D, dt_code, scale, sp),
+    }
+    reps = max(20, args.steps)
+    kern_us = {}
+    for name, fn in launches.items():
+        for _ in range(5):
+            check(fn())
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(reps):
+            check(fn())
+        e1.record(stream)
+        e1.synchronize()
+        kern_us[name] = e0.elapsed_time(e1) * 1e3 / reps
+
+    e = 2  # bytes per 16-bit element
+    pre_alg_bytes = 2 * B * H * T * D * e + 4 * B * H * T
+    pre_all_bytes = pre_alg_bytes + 4 * (B * H * T * D + 2 * B * KVH * T * D)
+    post_bytes = 4 * (B * H * T * D + 2 * B * KVH * T * D) + e * (B * H * T * D + 2 * B * KVH * T * D)
+    bwd_main_tflops = f_bwd / (kern_us["bwd_main"] * 1e-6) / 1e12
+    fwd_tflops = f_fwd / (kern_us["fwd"] * 1e-6) / 1e12
+
+    value = f_all / (ms * 1e-3) / 1e12
+    props = torch.cuda.get_device_properties(dev)
+    out = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": args.dtype,
+        "data": "synthetic",
+        "config": {
+            "workload": f"causal GQA attention fwd+bwd, B={B} T={T} {H}Q/{KVH}KV heads d={D} {args.dtype}, "
+            "one nanonemo::flash_attn + nanonemo::flash_attn_bwd call pair per step, HIP-graph replay",
+            "B": B, "T": T, "H": H, "KVH": KVH, "D": D,
+        },
+        "pct_of_bf16_peak": round(100 * value / PEAK_TFLOPS, 2),
+        "eager_ms_per_step": round(eager_ms, 5),
+        "roofline": {
+            "kernel": "fa_bwd_main_kernel",
+            "bound": "mfma",
+            "achieved": round(bwd_main_tflops, 2),
+            "peak": PEAK_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(bwd_main_tflops / PEAK_TFLOPS, 4),
+            "traffic": None,
+        },
+        "kernels": {
+            "fwd_us": round(kern_us["fwd"], 2),
+            "fwd_tflops": round(fwd_tflops, 2),
+            "bwd_pre_us": round(kern_us["bwd_pre"], 2),
+            "bwd_pre_alg_GBps": round(pre_alg_bytes / (kern_us["bwd_pre"] * 1e-6) / 1e9, 1),
+            "bwd_pre_moved_GBps": round(pre_all_bytes / (kern_us["bwd_pre"] * 1e-6) / 1e9, 1),
+            "bwd_main_us": round(kern_us["bwd_main"], 2),
+            "bwd_main_tflops": round(bwd_main_tflops, 2),
+            "bwd_post_us": round(kern_us["bwd_post"], 2),
+            "bwd_post_GBps": round(post_bytes / (kern_us["bwd_post"] * 1e-6) / 1e9, 1),
+        },
+        "device": {"name": props.name, "cus": props.multi_processor_count, "arch": getattr(props, "gcnArchName", "")},
+    }
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline(B, H, KVH, T, D, args.cpu_seconds)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

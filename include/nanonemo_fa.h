@@ -1,0 +1,84 @@
+/*
+ * nanonemo_fa.h — C ABI of the MI355X (gfx950) causal grouped-query FlashAttention-2 library
+ * (libnanonemo_fa.so, built from nanonemo_amd/csrc/flash_attn.hip).
+ *
+ * Contract shared by every entry point:
+ *   - Tensors are dense, contiguous, row-major device buffers:
+ *       q, o, dO, dq   [B, H,   T, D]   16-bit (dtype code below)
+ *       k, v, dk, dv   [B, KVH, T, D]   16-bit
+ *       lse            [B, H,   T]      fp32, natural-log logsumexp of the scaled scores
+ *   - Query head h reads KV head h / (H / KVH) (the order of repeat_interleave over heads).
+ *   - Causal, top-left aligned, square: key j is visible to query i iff j <= i.
+ *   - dtype: 0 = fp16, 1 = bf16. Operands are multiplied on MFMA with fp32 accumulation;
+ *     softmax statistics are fp32.
+ *   - D must be 32 or 64; H % KVH == 0; every pointer 16-byte aligned.
+ *   - `stream` is a hipStream_t (may be NULL for the default stream). Work is only enqueued:
+ *     no entry point allocates, frees, synchronises or reads device memory back to the host,
+ *     so every call may be captured into a HIP graph.
+ *   - Return value: 0 on success. Non-zero is an argument error (-1) or the hipError_t of a
+ *     failed launch; nn_fa_last_error() then returns the message (thread-local).
+ */
+#ifndef NANONEMO_FA_H
+#define NANONEMO_FA_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Forward: o = softmax(scale * q k^T + causal mask) v and lse per query row.
+ * Replaces the pybind `fwd(q, k, v) -> (o, lse)` of
+ * /root/reference/nanonemo/kernels/cuda/flash_attn.cu:362-379 (kernel :52-174),
+ * bound at /root/reference/nanonemo/kernels/cuda/flash_attn.py:18-22. */
+int nn_fa_fwd(const void* q, const void* k, const void* v, void* o, float* lse,
+              int64_t B, int64_t H, int64_t KVH, int64_t T, int64_t D,
+              int dtype, float scale, void* stream);
+
+/* Bytes of device workspace nn_fa_bwd needs (fp32 dQ/dK/dV accumulators and the
+ * D = rowsum(dO * o) vector). The caller allocates it; its contents on entry do not matter. */
+size_t nn_fa_bwd_workspace_size(int64_t B, int64_t H, int64_t KVH, int64_t T, int64_t D);
+
+/* Backward: (dq, dk, dv) in the input dtype, contiguous. dk/dv hold the sum over the
+ * H / KVH query heads that share each KV head. Runs nn_fa_bwd_pre, nn_fa_bwd_main and
+ * nn_fa_bwd_post in that order on `stream`.
+ * Replaces the pybind `bwd(d_o, q, k, v, o, lse) -> (dq, dk, dv)` of
+ * /root/reference/nanonemo/kernels/cuda/flash_attn.cu:381-405 (kernel :176-340),
+ * bound at /root/reference/nanonemo/kernels/cuda/flash_attn.py:31-35. */
+int nn_fa_bwd(const void* dO, const void* q, const void* k, const void* v, const void* o,
+              const float* lse, void* dq, void* dk, void* dv,
+              void* workspace, size_t workspace_bytes,
+              int64_t B, int64_t H, int64_t KVH, int64_t T, int64_t D,
+              int dtype, float scale, void* stream);
+
+/* Backward, stage 1: D = rowsum(dO * o) in fp32 and zeroed fp32 dQ/dK/dV accumulators.
+ * Replaces the ATen preprocessing inside flash_bwd, flash_attn.cu:387-391. */
+int nn_fa_bwd_pre(const void* o, const void* dO, void* workspace, size_t workspace_bytes,
+                  int64_t B, int64_t H, int64_t KVH, int64_t T, int64_t D, int dtype, void* stream);
+
+/* Backward, stage 2: recompute P from lse, accumulate dQ, dK, dV (fp32) into the workspace.
+ * Replaces bwd_kernel<HD>, flash_attn.cu:176-340 and its launch at :393-401. */
+int nn_fa_bwd_main(const void* q, const void* k, const void* v, const void* dO, const float* lse,
+                   void* workspace, size_t workspace_bytes,
+                   int64_t B, int64_t H, int64_t KVH, int64_t T, int64_t D,
+                   int dtype, float scale, void* stream);
+
+/* Backward, stage 3: scale and round the fp32 accumulators into dq, dk, dv.
+ * Replaces the three `.to(kFloat16)` casts of flash_attn.cu:404. */
+int nn_fa_bwd_post(const void* workspace, size_t workspace_bytes, void* dq, void* dk, void* dv,
+                   int64_t B, int64_t H, int64_t KVH, int64_t T, int64_t D,
+                   int dtype, float scale, void* stream);
+
+/* Message of the last failed call on this thread ("" if none). Replaces the TORCH_CHECK
+ * messages of flash_attn.cu:342-356 and :383-385. */
+const char* nn_fa_last_error(void);
+
+/* ABI version of this header (bumped on any signature change). */
+int nn_fa_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NANONEMO_FA_H */

@@ -1,0 +1,70 @@
+"""Ahead-of-time build of the HIP library for gfx950.
+
+Replaces the reference's JIT build (/root/reference/nanonemo/kernels/cuda/__init__.py:15-18, which runs
+nvcc through torch.utils.cpp_extension.load on first use): here ``hipcc`` compiles
+``nanonemo_amd/csrc/*.hip`` once, in-tree, into ``nanonemo_amd/lib/libnanonemo_fa.so``, a plain C-ABI
+shared library with no torch types in its signatures (include/nanonemo_fa.h). The library is loaded
+with ctypes (nanonemo_amd/kernels/hip/__init__.py), so the same .so runs on any box with the ROCm
+runtime.
+
+    python -m nanonemo_amd.build
+"""
+
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+ROOT = PKG.parent
+SRC = PKG / "csrc" / "flash_attn.hip"
+LIB_DIR = PKG / "lib"
+LIB = LIB_DIR / "libnanonemo_fa.so"
+ARCH = "gfx950"
+
+# -packed-fp32-ops: keep v_pk_{add,mul,fma}_f32 out of the generated code (those packed forms have
+# produced intermittent wrong results on the target boxes). hipcc's host pass warns that it does not
+# know the feature; that warning is harmless.
+HIPCC_FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-shared",
+    "-fPIC",
+    "-Xclang",
+    "-target-feature",
+    "-Xclang",
+    "-packed-fp32-ops",
+]
+
+
+def hipcc() -> str:
+    for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
+        if cand and Path(cand).exists():
+            return cand
+    raise RuntimeError("hipcc not found (looked at $HIPCC, /opt/rocm/bin/hipcc and PATH)")
+
+
+def build(verbose: bool = False) -> Path:
+    """Compile the HIP library (always recompiles) and return its path."""
+    LIB_DIR.mkdir(parents=True, exist_ok=True)
+    tmp = LIB.with_suffix(".so.tmp")
+    cmd = [hipcc(), *HIPCC_FLAGS, f"-I{ROOT / 'include'}", "-o", str(tmp), str(SRC)]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    noise = "'-packed-fp32-ops' is not a recognized feature"
+    log = "\n".join(l for l in (res.stdout + res.stderr).splitlines() if noise not in l)
+    if res.returncode != 0:
+        raise RuntimeError(f"hipcc failed ({res.returncode}):\n{log}")
+    if verbose and log.strip():
+        print(log, flush=True)
+    os.replace(tmp, LIB)  # atomic: a process that already mapped the old file keeps it
+    return LIB
+
+
+if __name__ == "__main__":
+    print(build(verbose="-q" not in sys.argv))

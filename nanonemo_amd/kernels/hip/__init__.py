@@ -1,0 +1,69 @@
+"""ctypes binding of the gfx950 HIP library (libnanonemo_fa.so, C ABI in include/nanonemo_fa.h).
+
+Replaces the reference's ``build(name)`` (/root/reference/nanonemo/kernels/cuda/__init__.py:15-18), which
+JIT-compiled a pybind11 torch extension. Here the library is built ahead of time by
+``nanonemo_amd.build`` and only loaded: no compiler runs on first use, and no torch type crosses the
+boundary (raw device pointers, int64 sizes, a dtype code, the scale and a hipStream_t).
+
+There is no fallback: if the library is missing, :func:`lib` raises, so a GPU run can never silently
+use another implementation.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from functools import cache
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parents[2] / "lib" / "libnanonemo_fa.so"
+
+DTYPE_F16 = 0
+DTYPE_BF16 = 1
+
+_i64 = ctypes.c_int64
+_vp = ctypes.c_void_p
+_int = ctypes.c_int
+_f32 = ctypes.c_float
+_sz = ctypes.c_size_t
+
+# name -> (restype, argtypes); must match include/nanonemo_fa.h
+SIGNATURES: dict[str, tuple] = {
+    "nn_fa_fwd": (_int, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _int, _f32, _vp]),
+    "nn_fa_bwd_workspace_size": (_sz, [_i64, _i64, _i64, _i64, _i64]),
+    "nn_fa_bwd": (
+        _int,
+        [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _i64, _i64, _i64, _i64, _i64, _int, _f32, _vp],
+    ),
+    "nn_fa_bwd_pre": (_int, [_vp, _vp, _vp, _sz, _i64, _i64, _i64, _i64, _i64, _int, _vp]),
+    "nn_fa_bwd_main": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _sz, _i64, _i64, _i64, _i64, _i64, _int, _f32, _vp]),
+    "nn_fa_bwd_post": (_int, [_vp, _sz, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _int, _f32, _vp]),
+    "nn_fa_last_error": (ctypes.c_char_p, []),
+    "nn_fa_abi_version": (_int, []),
+}
+
+ABI_VERSION = 1
+
+
+@cache
+def lib() -> ctypes.CDLL:
+    """Load libnanonemo_fa.so once per process and declare every entry point's C signature."""
+    if not LIB_PATH.exists():
+        raise RuntimeError(
+            f"HIP library {LIB_PATH} is not built; run `python -m nanonemo_amd.build` "
+            "(or __graft_entry__.build()) first. There is no non-HIP fallback."
+        )
+    handle = ctypes.CDLL(str(LIB_PATH))
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(handle, name)
+        fn.restype = res
+        fn.argtypes = args
+    if handle.nn_fa_abi_version() != ABI_VERSION:
+        raise RuntimeError(f"{LIB_PATH} has ABI {handle.nn_fa_abi_version()}, expected {ABI_VERSION}; rebuild it")
+    return handle
+
+
+def check(rc: int) -> None:
+    """Raise RuntimeError with the library's message when an entry point returns non-zero."""
+    if rc != 0:
+        msg = lib().nn_fa_last_error().decode(errors="replace")
+        raise RuntimeError(msg or f"nanonemo_fa call failed with code {rc}")

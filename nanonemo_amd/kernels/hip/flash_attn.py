@@ -1,0 +1,138 @@
+"""torch.library boundary of the gfx950 causal GQA FlashAttention-2 kernels.
+
+Drop-in for /root/reference/nanonemo/kernels/cuda/flash_attn.py: the same op names and schemas
+(``nanonemo::flash_attn`` :18-22 and ``nanonemo::flash_attn_bwd`` :31-35), the same fake impls
+(contiguous outputs, :25-28 and :38-40), the same autograd wiring (save q, k, v, o, lse; ignore the
+gradient of lse, :43-54) and the same public ``flash_attn(q, k, v) -> o`` (:57-60). Under
+``torch.compile(fullgraph=True)`` each op is one opaque node traced through its fake impl.
+
+Differences from the reference, all widening: fp16 **and** bf16 inputs (the reference accepts fp16
+only, flash_attn.cu:344-346), and the compute is the HIP library behind a C ABI
+(include/nanonemo_fa.h) called through ctypes on PyTorch's current HIP stream. Every output and the
+backward workspace is allocated here by PyTorch's caching allocator; the library never allocates,
+synchronises or copies to the host, so both ops can be captured into a HIP graph.
+"""
+
+from __future__ import annotations
+
+import math
+
+import torch
+from torch import Tensor
+
+from nanonemo_amd.kernels.hip import DTYPE_BF16, DTYPE_F16, check, lib
+
+_DTYPES = {torch.float16: DTYPE_F16, torch.bfloat16: DTYPE_BF16}
+
+
+def _check_inputs(q: Tensor, k: Tensor, v: Tensor) -> None:
+    """The reference's check_inputs (flash_attn.cu:342-356) with the dtype set widened to {fp16, bf16}."""
+    if not (q.is_cuda and k.is_cuda and v.is_cuda):
+        raise RuntimeError("inputs must be CUDA tensors")
+    if q.dtype not in _DTYPES or k.dtype != q.dtype or v.dtype != q.dtype:
+        raise RuntimeError("inputs must be float16 or bfloat16 (all the same dtype)")
+    if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
+        raise RuntimeError("expected (B, H, T, hd) / (B, KVH, T, hd)")
+    if not (q.is_contiguous() and k.is_contiguous() and v.is_contiguous()):
+        raise RuntimeError("inputs must be contiguous")
+    if q.size(0) != k.size(0) or q.size(2) != k.size(2) or k.shape != v.shape:
+        raise RuntimeError("K and V must share shape; Q must share batch and length")
+    if q.size(3) != k.size(3):
+        raise RuntimeError("Q and K must share head_dim")
+    if q.size(3) not in (32, 64):
+        raise RuntimeError("head_dim must be 32 or 64")
+    if k.size(1) == 0 or q.size(1) % k.size(1) != 0:
+        raise RuntimeError("query heads must group evenly over KV heads")
+    if q.device != k.device or q.device != v.device:
+        raise RuntimeError("inputs must be on the same device")
+    for t in (q, k, v):
+        if t.numel() and t.data_ptr() % 16 != 0:
+            raise RuntimeError("inputs must be 16-byte aligned")
+
+
+def _stream(t: Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _contig(t: Tensor) -> Tensor:
+    return t if t.is_contiguous() else t.contiguous()
+
+
+@torch.library.custom_op("nanonemo::flash_attn", mutates_args=())
+def _flash_attn(q: Tensor, k: Tensor, v: Tensor) -> tuple[Tensor, Tensor]:
+    q, k, v = _contig(q), _contig(k), _contig(v)
+    _check_inputs(q, k, v)
+    B, H, T, D = q.shape
+    o = torch.empty_like(q, memory_format=torch.contiguous_format)
+    lse = torch.empty((B, H, T), dtype=torch.float32, device=q.device)
+    if B == 0 or T == 0 or H == 0:
+        return o, lse
+    with torch.cuda.device(q.device):
+        rc = lib().nn_fa_fwd(
+            q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(),
+            B, H, k.size(1), T, D, _DTYPES[q.dtype], 1.0 / math.sqrt(D), _stream(q),
+        )
+    check(rc)
+    return o, lse
+
+
+@_flash_attn.register_fake
+def _(q, k, v):
+    B, H, T, _ = q.shape  # the kernel returns contiguous tensors whatever the input strides
+    return (
+        torch.empty(q.shape, dtype=q.dtype, device=q.device),
+        torch.empty((B, H, T), dtype=torch.float32, device=q.device),
+    )
+
+
+@torch.library.custom_op("nanonemo::flash_attn_bwd", mutates_args=())
+def _flash_attn_bwd(d_o: Tensor, q: Tensor, k: Tensor, v: Tensor, o: Tensor, lse: Tensor) -> tuple[Tensor, Tensor, Tensor]:
+    d_o, q, k, v, o, lse = (_contig(t) for t in (d_o, q, k, v, o, lse))
+    _check_inputs(q, k, v)
+    if d_o.shape != q.shape or d_o.dtype != q.dtype or o.shape != q.shape or o.dtype != q.dtype:
+        raise RuntimeError("d_o must be a contiguous float16/bfloat16 tensor shaped like q")
+    B, H, T, D = q.shape
+    KVH = k.size(1)
+    if lse.shape != (B, H, T) or lse.dtype != torch.float32:
+        raise RuntimeError("lse must be a float32 tensor of shape (B, H, T)")
+    dq = torch.empty_like(q, memory_format=torch.contiguous_format)
+    dk = torch.empty_like(k, memory_format=torch.contiguous_format)
+    dv = torch.empty_like(v, memory_format=torch.contiguous_format)
+    if B == 0 or T == 0 or H == 0:
+        return dq, dk, dv
+    L = lib()
+    ws_bytes = L.nn_fa_bwd_workspace_size(B, H, KVH, T, D)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device)
+    with torch.cuda.device(q.device):
+        rc = L.nn_fa_bwd(
+            d_o.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(),
+            dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), ws.data_ptr(), ws_bytes,
+            B, H, KVH, T, D, _DTYPES[q.dtype], 1.0 / math.sqrt(D), _stream(q),
+        )
+    check(rc)
+    return dq, dk, dv
+
+
+@_flash_attn_bwd.register_fake
+def _(d_o, q, k, v, o, lse):
+    return tuple(torch.empty(t.shape, dtype=t.dtype, device=t.device) for t in (q, k, v))
+
+
+def _setup_context(ctx, inputs, output):
+    q, k, v = inputs
+    o, lse = output
+    ctx.save_for_backward(q, k, v, o, lse)
+
+
+def _backward(ctx, d_o, _d_lse):
+    q, k, v, o, lse = ctx.saved_tensors
+    return _flash_attn_bwd(d_o, q, k, v, o, lse)
+
+
+_flash_attn.register_autograd(_backward, setup_context=_setup_context)
+
+
+def flash_attn(q: Tensor, k: Tensor, v: Tensor) -> Tensor:
+    """Causal GQA attention. q: (B, H, T, hd), k/v: (B, KVH, T, hd), fp16 or bf16, H % KVH == 0, hd in {32, 64}."""
+    o, _ = _flash_attn(q, k, v)
+    return o

@@ -1,0 +1,146 @@
+"""CPU tests of the drop-in boundary: the C-ABI library, its exports, its argument checks, and the
+torch.library ops' schemas, fake impls and input validation. No GPU compute is launched here."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+from nanonemo_amd.kernels.hip import ABI_VERSION, LIB_PATH, SIGNATURES, lib
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "nanonemo_fa.h"
+
+
+def _declared_symbols() -> list[str]:
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(nn_fa_\w+)\s*\(", text)))
+
+
+def test_library_is_built():
+    assert LIB_PATH.exists(), "run `python -m nanonemo_amd.build` (or __graft_entry__.build()) first"
+
+
+def test_library_exports_every_header_symbol():
+    handle = ctypes.CDLL(str(LIB_PATH))
+    declared = _declared_symbols()
+    assert declared, "no declarations parsed from the header"
+    for name in declared:
+        assert hasattr(handle, name), f"{name} declared in {HEADER.name} but not exported"
+    # and the Python binding declares a signature for each of them
+    assert sorted(SIGNATURES) == declared
+
+
+def test_abi_version():
+    assert lib().nn_fa_abi_version() == ABI_VERSION
+
+
+def test_workspace_size():
+    L = lib()
+    B, H, KVH, T, D = 8, 12, 4, 1024, 64
+    acc = 4 * (B * H * T * D + 2 * B * KVH * T * D)
+    dvec = 4 * B * H * T
+    rnd = lambda n: (n + 255) // 256 * 256  # noqa: E731
+    assert L.nn_fa_bwd_workspace_size(B, H, KVH, T, D) == rnd(acc) + rnd(dvec)
+    assert L.nn_fa_bwd_workspace_size(0, H, KVH, T, D) == 0
+
+
+@pytest.mark.parametrize(
+    "args, msg",
+    [
+        ((1, 4, 2, 16, 48, 1), "head_dim must be 32 or 64"),
+        ((1, 4, 3, 16, 64, 1), "query heads must group evenly"),
+        ((1, 4, 2, 16, 64, 7), "float16 or bfloat16"),
+        ((1, 4, 0, 16, 64, 1), "invalid sizes"),
+        ((-1, 4, 2, 16, 64, 1), "invalid sizes"),
+    ],
+)
+def test_c_abi_rejects_bad_arguments_before_any_launch(args, msg):
+    L = lib()
+    B, H, KVH, T, D, dt = args
+    rc = L.nn_fa_fwd(16, 16, 16, 16, 16, B, H, KVH, T, D, dt, 0.125, None)
+    assert rc != 0
+    assert msg in L.nn_fa_last_error().decode()
+    rc = L.nn_fa_bwd(16, 16, 16, 16, 16, 16, 16, 16, 16, 256, 1 << 30, B, H, KVH, T, D, dt, 0.125, None)
+    assert rc != 0 and msg in L.nn_fa_last_error().decode()
+
+
+def test_c_abi_rejects_misaligned_and_small_workspace():
+    L = lib()
+    rc = L.nn_fa_fwd(8, 16, 16, 16, 16, 1, 4, 2, 16, 64, 1, 0.125, None)
+    assert rc != 0 and "16-byte aligned" in L.nn_fa_last_error().decode()
+    rc = L.nn_fa_bwd_main(16, 16, 16, 16, 16, 256, 10, 1, 4, 2, 16, 64, 1, 0.125, None)
+    assert rc != 0 and "workspace too small" in L.nn_fa_last_error().decode()
+    rc = L.nn_fa_bwd_pre(16, 16, 0, 1 << 20, 1, 4, 2, 16, 64, 1, None)
+    assert rc != 0 and "null workspace" in L.nn_fa_last_error().decode()
+
+
+def test_c_abi_empty_problem_is_a_no_op():
+    # T == 0 and B == 0 return success without touching device memory (flash_attn.cu:367).
+    L = lib()
+    assert L.nn_fa_fwd(None, None, None, None, None, 1, 4, 2, 0, 64, 1, 0.125, None) == 0
+    assert L.nn_fa_fwd(None, None, None, None, None, 0, 4, 2, 16, 64, 1, 0.125, None) == 0
+    assert L.nn_fa_last_error().decode() == ""
+
+
+# ---- torch.library ops -----------------------------------------------------------------------
+
+
+def _ops():
+    from nanonemo_amd.kernels.hip import flash_attn as fa
+
+    return fa
+
+
+def test_ops_registered_with_reference_schemas():
+    _ops()
+    fwd = torch.ops.nanonemo.flash_attn.default._schema
+    bwd = torch.ops.nanonemo.flash_attn_bwd.default._schema
+    assert str(fwd) == "nanonemo::flash_attn(Tensor q, Tensor k, Tensor v) -> (Tensor, Tensor)"
+    assert str(bwd) == (
+        "nanonemo::flash_attn_bwd(Tensor d_o, Tensor q, Tensor k, Tensor v, Tensor o, Tensor lse)"
+        " -> (Tensor, Tensor, Tensor)"
+    )
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_fake_impls_give_contiguous_outputs_for_strided_inputs(dtype):
+    fa = _ops()
+    B, H, KVH, T, D = 2, 12, 4, 64, 64
+    q = torch.empty(B, T, H, D, dtype=dtype, device="meta").transpose(1, 2)
+    k = torch.empty(B, T, KVH, D, dtype=dtype, device="meta").transpose(1, 2)
+    v = torch.empty(B, KVH, T, D, dtype=dtype, device="meta")
+    assert not q.is_contiguous()
+    o, lse = torch.ops.nanonemo.flash_attn(q, k, v)
+    assert o.shape == q.shape and o.dtype == dtype and o.is_contiguous()
+    assert lse.shape == (B, H, T) and lse.dtype == torch.float32 and lse.is_contiguous()
+    dq, dk, dv = torch.ops.nanonemo.flash_attn_bwd(o, q, k, v, o, lse)
+    for g, t in ((dq, q), (dk, k), (dv, v)):
+        assert g.shape == t.shape and g.dtype == t.dtype and g.is_contiguous()
+    assert fa.flash_attn(q, k, v).shape == q.shape
+
+
+@pytest.mark.parametrize(
+    "make, msg",
+    [
+        (lambda: [torch.zeros(1, 4, 8, 64, dtype=torch.float16)] * 3, "inputs must be CUDA tensors"),
+    ],
+)
+def test_op_rejects_cpu_tensors(make, msg):
+    fa = _ops()
+    q, k, v = make()
+    with pytest.raises(RuntimeError, match=msg):
+        fa.flash_attn(q, k, v)
+
+
+def test_product_never_imports_the_oracle():
+    pkg = ROOT / "nanonemo_amd"
+    for path in pkg.rglob("*"):
+        if path.suffix in {".py", ".hip", ".h", ".cpp"}:
+            text = path.read_text()
+            assert not re.search(r"^\s*(from|import)\s+oracle\b", text, re.M), path
+            assert "oracle/" not in text, path
