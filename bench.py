@@ -2,12 +2,13 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--dtype bf16|fp16] [--batch 8] [--seq 1024]
 
-A step is one call pair through the torch.library boundary, ``nanonemo::flash_attn`` then
-``nanonemo::flash_attn_bwd`` (what autograd runs per attention layer), on synthetic N(0,1) inputs
-already resident in HBM. Default workload: B=8, T=1024, 12 query / 4 KV heads, head_dim 64, bf16 (the
-north-star shape of BASELINE.json). The step is captured once into a HIP graph (as the reference's
-benchmark does, /root/reference/benchmarks/kernels/common.py:30-54) and K replays are timed between
-device synchronisations; the eager (uncaptured) time per step is reported beside it.
+A step is one forward + backward of the hot path through the drop-in C ABI (nn_fa_fwd then nn_fa_bwd,
+include/nanonemo_fa.h) on synthetic N(0,1) inputs already resident in HBM, with outputs and the backward
+workspace allocated once. Default workload: B=8, T=1024, 12 query / 4 KV heads, head_dim 64, bf16 (the
+north-star shape of BASELINE.json). W untimed steps, then K timed steps between device
+synchronisations. The same pair through the torch.library ops (nanonemo::flash_attn +
+nanonemo::flash_attn_bwd, which add output allocation and Python dispatch) is timed beside it as
+op_ms_per_step.
 
 value = algorithmic FLOPs per step / time per step, with F_alg = 6*B*H*D*T*(T+1) (12*D flop per causal
 (query, key) pair: 2 forward and 4 backward products; the backward's recompute of S is not counted).
@@ -55,7 +56,7 @@ def parse():
     p.add_argument("--head-dim", type=int, default=64)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="budget of the CPU baseline sample")
-    p.add_argument("--profile-only", action="store_true", help="only the timed graph replays (for rocprofv3)")
+    p.add_argument("--profile-only", action="store_true", help="only the timed steps (for rocprofv3)")
     return p.parse_args()
 
 
@@ -138,57 +139,53 @@ def main():
     v = torch.randn(B, KVH, T, D, device=dev).to(dtype)
     do = torch.randn(B, H, T, D, device=dev).to(dtype)
 
-    def step():
-        o, lse = fa._flash_attn(q, k, v)
-        return fa._flash_attn_bwd(do, q, k, v, o, lse)
-
-    # ---- eager steps (warm-up W, then K timed) ----
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        step()
-    torch.cuda.synchronize()
-    eager_ms = (time.perf_counter() - t0) * 1e3 / args.steps
-
-    # ---- graph-captured step, K timed replays ----
-    side = torch.cuda.Stream()
-    side.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(side):
-        for _ in range(3):
-            step()
-    torch.cuda.current_stream().wait_stream(side)
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        step()
-    for _ in range(args.warmup):
-        graph.replay()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        graph.replay()
-    torch.cuda.synchronize()
-    ms = (time.perf_counter() - t0) * 1e3 / args.steps
-    if args.profile_only:
-        print(json.dumps({"ms_per_step": ms, "eager_ms_per_step": eager_ms}), flush=True)
-        return
-
-    # ---- each kernel alone, HIP events on the launch stream ----
     L = lib()
     dt_code = DTYPE_BF16 if dtype == torch.bfloat16 else DTYPE_F16
     stream = torch.cuda.current_stream()
     sp = stream.cuda_stream
-    o, lse = fa._flash_attn(q, k, v)
+    o = torch.empty_like(q)
+    lse = torch.empty(B, H, T, dtype=torch.float32, device=dev)
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
     ws_bytes = L.nn_fa_bwd_workspace_size(B, H, KVH, T, D)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
-    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    ptr = {n: t.data_ptr() for n, t in dict(q=q, k=k, v=v, do=do, o=o, lse=lse, dq=dq, dk=dk, dv=dv, ws=ws).items()}
+
+    def step_abi():
+        """One fwd+bwd through the C ABI (the drop-in boundary) with outputs already allocated."""
+        check(L.nn_fa_fwd(ptr["q"], ptr["k"], ptr["v"], ptr["o"], ptr["lse"], B, H, KVH, T, D, dt_code, scale, sp))
+        check(L.nn_fa_bwd(ptr["do"], ptr["q"], ptr["k"], ptr["v"], ptr["o"], ptr["lse"], ptr["dq"], ptr["dk"],
+                          ptr["dv"], ptr["ws"], ws_bytes, B, H, KVH, T, D, dt_code, scale, sp))
+
+    def step_op():
+        """The same pair through the torch.library ops (allocates outputs with the caching allocator)."""
+        o2, lse2 = fa._flash_attn(q, k, v)
+        return fa._flash_attn_bwd(do, q, k, v, o2, lse2)
+
+    def timed(fn, n):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(n):
+            fn()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) * 1e3 / n
+
+    for _ in range(args.warmup):
+        step_abi()
+        step_op()
+    # The headline: K steps through the C ABI, bracketed by device synchronisations.
+    ms = timed(step_abi, args.steps)
+    op_ms = timed(step_op, args.steps)
+    if args.profile_only:
+        print(json.dumps({"ms_per_step": ms, "op_ms_per_step": op_ms}), flush=True)
+        return
+
+    # ---- each kernel alone, HIP events on the launch stream ----
     launches = {
         "fwd": lambda: L.nn_fa_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(),
                                    B, H, KVH, T, D, dt_code, scale, sp),
-        "bwd_pre": lambda: L.nn_fa_bwd_pre(o.data_ptr(), do.data_ptr(), ws.data_ptr(), ws_bytes,
+        "bwd_pre": lambda: L.nn_fa_bwd_pre(o.data_ptr(), do.data_ptr(), lse.data_ptr(), ws.data_ptr(), ws_bytes,
                                            B, H, KVH, T, D, dt_code, sp),
-        "bwd_main": lambda: L.nn_fa_bwd_main(q.data_ptr(), k.data_ptr(), v.data_ptr(), do.data_ptr(), lse.data_ptr(),
+        "bwd_main": lambda: L.nn_fa_bwd_main(q.data_ptr(), k.data_ptr(), v.data_ptr(), do.data_ptr(),
                                              ws.data_ptr(), ws_bytes, B, H, KVH, T, D, dt_code, scale, sp),
         "bwd_post": lambda: L.nn_fa_bwd_post(ws.data_ptr(), ws_bytes, dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
                                              B, H, KVH, T, D, dt_code, scale, sp),
@@ -208,7 +205,8 @@ def main():
 
     e = 2  # bytes per 16-bit element
     pre_alg_bytes = 2 * B * H * T * D * e + 4 * B * H * T
-    pre_all_bytes = pre_alg_bytes + 4 * (B * H * T * D + 2 * B * KVH * T * D)
+    # also reads lse, writes its base-2 copy and zeroes the fp32 accumulators
+    pre_all_bytes = pre_alg_bytes + 8 * B * H * T + 4 * (B * H * T * D + 2 * B * KVH * T * D)
     post_bytes = 4 * (B * H * T * D + 2 * B * KVH * T * D) + e * (B * H * T * D + 2 * B * KVH * T * D)
     bwd_main_tflops = f_bwd / (kern_us["bwd_main"] * 1e-6) / 1e12
     fwd_tflops = f_fwd / (kern_us["fwd"] * 1e-6) / 1e12
@@ -230,11 +228,11 @@ def main():
         "data": "synthetic",
         "config": {
             "workload": f"causal GQA attention fwd+bwd, B={B} T={T} {H}Q/{KVH}KV heads d={D} {args.dtype}, "
-            "one nanonemo::flash_attn + nanonemo::flash_attn_bwd call pair per step, HIP-graph replay",
+            "one nn_fa_fwd + nn_fa_bwd C-ABI call pair per step on resident inputs",
             "B": B, "T": T, "H": H, "KVH": KVH, "D": D,
         },
         "pct_of_bf16_peak": round(100 * value / PEAK_TFLOPS, 2),
-        "eager_ms_per_step": round(eager_ms, 5),
+        "op_ms_per_step": round(op_ms, 5),
         "roofline": {
             "kernel": "fa_bwd_main_kernel",
             "bound": "mfma",

@@ -36,8 +36,9 @@ int nn_fa_fwd(const void* q, const void* k, const void* v, void* o, float* lse,
               int64_t B, int64_t H, int64_t KVH, int64_t T, int64_t D,
               int dtype, float scale, void* stream);
 
-/* Bytes of device workspace nn_fa_bwd needs (fp32 dQ/dK/dV accumulators and the
- * D = rowsum(dO * o) vector). The caller allocates it; its contents on entry do not matter. */
+/* Bytes of device workspace nn_fa_bwd needs (fp32 dQ/dK/dV accumulators, the D = rowsum(dO * o)
+ * vector and a base-2 copy of lse). The caller allocates it, 256-byte aligned; its contents on
+ * entry do not matter. */
 size_t nn_fa_bwd_workspace_size(int64_t B, int64_t H, int64_t KVH, int64_t T, int64_t D);
 
 /* Backward: (dq, dk, dv) in the input dtype, contiguous. dk/dv hold the sum over the
@@ -52,14 +53,16 @@ int nn_fa_bwd(const void* dO, const void* q, const void* k, const void* v, const
               int64_t B, int64_t H, int64_t KVH, int64_t T, int64_t D,
               int dtype, float scale, void* stream);
 
-/* Backward, stage 1: D = rowsum(dO * o) in fp32 and zeroed fp32 dQ/dK/dV accumulators.
+/* Backward, stage 1: D = rowsum(dO * o) and lse * log2(e) in fp32, and zeroed fp32 dQ/dK/dV
+ * accumulators, all in the workspace.
  * Replaces the ATen preprocessing inside flash_bwd, flash_attn.cu:387-391. */
-int nn_fa_bwd_pre(const void* o, const void* dO, void* workspace, size_t workspace_bytes,
+int nn_fa_bwd_pre(const void* o, const void* dO, const float* lse, void* workspace, size_t workspace_bytes,
                   int64_t B, int64_t H, int64_t KVH, int64_t T, int64_t D, int dtype, void* stream);
 
-/* Backward, stage 2: recompute P from lse, accumulate dQ, dK, dV (fp32) into the workspace.
+/* Backward, stage 2: recompute P from the workspace's lse, accumulate dQ, dK, dV (fp32) into
+ * the workspace. Needs the workspace prepared by nn_fa_bwd_pre.
  * Replaces bwd_kernel<HD>, flash_attn.cu:176-340 and its launch at :393-401. */
-int nn_fa_bwd_main(const void* q, const void* k, const void* v, const void* dO, const float* lse,
+int nn_fa_bwd_main(const void* q, const void* k, const void* v, const void* dO,
                    void* workspace, size_t workspace_bytes,
                    int64_t B, int64_t H, int64_t KVH, int64_t T, int64_t D,
                    int dtype, float scale, void* stream);

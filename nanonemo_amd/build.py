@@ -38,6 +38,10 @@ HIPCC_FLAGS = [
     "-target-feature",
     "-Xclang",
     "-packed-fp32-ops",
+    # MFMA accumulators in ordinary VGPRs: without this the compiler parks them in AGPRs and
+    # copies every element through v_accvgpr_read/write around each softmax step.
+    "-mllvm",
+    "-amdgpu-mfma-vgpr-form=1",
 ]
 
 
