@@ -14,9 +14,10 @@ value = algorithmic FLOPs per step / time per step, with F_alg = 6*B*H*D*T*(T+1)
 (query, key) pair: 2 forward and 4 backward products; the backward's recompute of S is not counted).
 
 The JSON line also carries:
-  roofline      the dominant kernel (the backward main kernel), timed alone with HIP events on the
-                stream it is launched on: achieved = its algorithmic FLOPs (8*D per causal pair) per
-                launch / its mean launch time, against the dense BF16/FP16 MFMA peak of 2.5 PFLOP/s;
+  roofline      the dominant kernel (the longest of the forward, dK/dV and dQ kernels), timed alone
+                with HIP events on the stream it is launched on: achieved = its algorithmic FLOPs per
+                launch (forward 4*D, dK/dV 6*D, dQ 2*D per causal pair) / its mean launch time, against
+                the dense BF16/FP16 MFMA peak of 2.5 PFLOP/s;
   cpu_baseline  the reference's plain-PyTorch attention (repeat_interleave + SDPA math, forward +
                 autograd) in fp32 on the host cores, on a bounded sample of the same workload;
   kernels       per-kernel mean times and the preprocessing pass's HBM rate.
@@ -185,10 +186,10 @@ def main():
                                    B, H, KVH, T, D, dt_code, scale, sp),
         "bwd_pre": lambda: L.nn_fa_bwd_pre(o.data_ptr(), do.data_ptr(), lse.data_ptr(), ws.data_ptr(), ws_bytes,
                                            B, H, KVH, T, D, dt_code, sp),
-        "bwd_main": lambda: L.nn_fa_bwd_main(q.data_ptr(), k.data_ptr(), v.data_ptr(), do.data_ptr(),
-                                             ws.data_ptr(), ws_bytes, B, H, KVH, T, D, dt_code, scale, sp),
-        "bwd_post": lambda: L.nn_fa_bwd_post(ws.data_ptr(), ws_bytes, dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
-                                             B, H, KVH, T, D, dt_code, scale, sp),
+        "bwd_dkdv": lambda: L.nn_fa_bwd_dkdv(q.data_ptr(), k.data_ptr(), v.data_ptr(), do.data_ptr(), ws.data_ptr(),
+                                             ws_bytes, dk.data_ptr(), dv.data_ptr(), B, H, KVH, T, D, dt_code, scale, sp),
+        "bwd_dq": lambda: L.nn_fa_bwd_dq(q.data_ptr(), k.data_ptr(), v.data_ptr(), do.data_ptr(), ws.data_ptr(),
+                                         ws_bytes, dq.data_ptr(), B, H, KVH, T, D, dt_code, scale, sp),
     }
     reps = max(20, args.steps)
     kern_us = {}
@@ -205,11 +206,18 @@ def main():
 
     e = 2  # bytes per 16-bit element
     pre_alg_bytes = 2 * B * H * T * D * e + 4 * B * H * T
-    # also reads lse, writes its base-2 copy and zeroes the fp32 accumulators
-    pre_all_bytes = pre_alg_bytes + 8 * B * H * T + 4 * (B * H * T * D + 2 * B * KVH * T * D)
-    post_bytes = 4 * (B * H * T * D + 2 * B * KVH * T * D) + e * (B * H * T * D + 2 * B * KVH * T * D)
-    bwd_main_tflops = f_bwd / (kern_us["bwd_main"] * 1e-6) / 1e12
-    fwd_tflops = f_fwd / (kern_us["fwd"] * 1e-6) / 1e12
+    pre_all_bytes = pre_alg_bytes + 8 * B * H * T  # also reads lse and writes its base-2 copy
+    # Algorithmic FLOPs (8*D per causal pair for the backward) split by the products each kernel owns:
+    # dV, dP, dK -> dk/dv kernel (6*D), dQ -> dq kernel (2*D); the dP and S recomputed by each are not counted.
+    f_dkdv = 3.0 * B * H * D * T * (T + 1)
+    f_dq = 1.0 * B * H * D * T * (T + 1)
+    kern_tflops = {
+        "fwd": f_fwd / (kern_us["fwd"] * 1e-6) / 1e12,
+        "bwd_dkdv": f_dkdv / (kern_us["bwd_dkdv"] * 1e-6) / 1e12,
+        "bwd_dq": f_dq / (kern_us["bwd_dq"] * 1e-6) / 1e12,
+    }
+    dominant = max(("fwd", "bwd_dkdv", "bwd_dq"), key=lambda n: kern_us[n])
+    kernel_names = {"fwd": "fa_fwd_kernel", "bwd_dkdv": "fa_bwd_dkdv_kernel", "bwd_dq": "fa_bwd_dq_kernel"}
 
     value = f_all / (ms * 1e-3) / 1e12
     props = torch.cuda.get_device_properties(dev)
@@ -234,24 +242,25 @@ def main():
         "pct_of_bf16_peak": round(100 * value / PEAK_TFLOPS, 2),
         "op_ms_per_step": round(op_ms, 5),
         "roofline": {
-            "kernel": "fa_bwd_main_kernel",
+            "kernel": kernel_names[dominant],
             "bound": "mfma",
-            "achieved": round(bwd_main_tflops, 2),
+            "achieved": round(kern_tflops[dominant], 2),
             "peak": PEAK_TFLOPS,
             "unit": "TFLOP/s",
-            "frac": round(bwd_main_tflops / PEAK_TFLOPS, 4),
+            "frac": round(kern_tflops[dominant] / PEAK_TFLOPS, 4),
             "traffic": None,
         },
         "kernels": {
             "fwd_us": round(kern_us["fwd"], 2),
-            "fwd_tflops": round(fwd_tflops, 2),
+            "fwd_tflops": round(kern_tflops["fwd"], 2),
             "bwd_pre_us": round(kern_us["bwd_pre"], 2),
             "bwd_pre_alg_GBps": round(pre_alg_bytes / (kern_us["bwd_pre"] * 1e-6) / 1e9, 1),
             "bwd_pre_moved_GBps": round(pre_all_bytes / (kern_us["bwd_pre"] * 1e-6) / 1e9, 1),
-            "bwd_main_us": round(kern_us["bwd_main"], 2),
-            "bwd_main_tflops": round(bwd_main_tflops, 2),
-            "bwd_post_us": round(kern_us["bwd_post"], 2),
-            "bwd_post_GBps": round(post_bytes / (kern_us["bwd_post"] * 1e-6) / 1e9, 1),
+            "bwd_dkdv_us": round(kern_us["bwd_dkdv"], 2),
+            "bwd_dkdv_tflops": round(kern_tflops["bwd_dkdv"], 2),
+            "bwd_dq_us": round(kern_us["bwd_dq"], 2),
+            "bwd_dq_tflops": round(kern_tflops["bwd_dq"], 2),
+            "bwd_tflops": round(f_bwd / ((kern_us["bwd_pre"] + kern_us["bwd_dkdv"] + kern_us["bwd_dq"]) * 1e-6) / 1e12, 2),
         },
         "device": {"name": props.name, "cus": props.multi_processor_count, "arch": getattr(props, "gcnArchName", "")},
     }

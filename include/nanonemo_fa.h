@@ -36,14 +36,14 @@ int nn_fa_fwd(const void* q, const void* k, const void* v, void* o, float* lse,
               int64_t B, int64_t H, int64_t KVH, int64_t T, int64_t D,
               int dtype, float scale, void* stream);
 
-/* Bytes of device workspace nn_fa_bwd needs (fp32 dQ/dK/dV accumulators, the D = rowsum(dO * o)
- * vector and a base-2 copy of lse). The caller allocates it, 256-byte aligned; its contents on
- * entry do not matter. */
+/* Bytes of device workspace the backward needs: D = rowsum(dO * o) and a base-2 copy of lse,
+ * one fp32 each per query row. The caller allocates it, 256-byte aligned; its contents on entry
+ * do not matter. */
 size_t nn_fa_bwd_workspace_size(int64_t B, int64_t H, int64_t KVH, int64_t T, int64_t D);
 
 /* Backward: (dq, dk, dv) in the input dtype, contiguous. dk/dv hold the sum over the
- * H / KVH query heads that share each KV head. Runs nn_fa_bwd_pre, nn_fa_bwd_main and
- * nn_fa_bwd_post in that order on `stream`.
+ * H / KVH query heads that share each KV head. Runs nn_fa_bwd_pre, nn_fa_bwd_dkdv and
+ * nn_fa_bwd_dq in that order on `stream`. Deterministic: no atomics.
  * Replaces the pybind `bwd(d_o, q, k, v, o, lse) -> (dq, dk, dv)` of
  * /root/reference/nanonemo/kernels/cuda/flash_attn.cu:381-405 (kernel :176-340),
  * bound at /root/reference/nanonemo/kernels/cuda/flash_attn.py:31-35. */
@@ -53,25 +53,24 @@ int nn_fa_bwd(const void* dO, const void* q, const void* k, const void* v, const
               int64_t B, int64_t H, int64_t KVH, int64_t T, int64_t D,
               int dtype, float scale, void* stream);
 
-/* Backward, stage 1: D = rowsum(dO * o) and lse * log2(e) in fp32, and zeroed fp32 dQ/dK/dV
- * accumulators, all in the workspace.
+/* Backward, stage 1: D = rowsum(dO * o) and lse * log2(e), fp32, into the workspace.
  * Replaces the ATen preprocessing inside flash_bwd, flash_attn.cu:387-391. */
 int nn_fa_bwd_pre(const void* o, const void* dO, const float* lse, void* workspace, size_t workspace_bytes,
                   int64_t B, int64_t H, int64_t KVH, int64_t T, int64_t D, int dtype, void* stream);
 
-/* Backward, stage 2: recompute P from the workspace's lse, accumulate dQ, dK, dV (fp32) into
- * the workspace. Needs the workspace prepared by nn_fa_bwd_pre.
- * Replaces bwd_kernel<HD>, flash_attn.cu:176-340 and its launch at :393-401. */
-int nn_fa_bwd_main(const void* q, const void* k, const void* v, const void* dO,
-                   void* workspace, size_t workspace_bytes,
+/* Backward, stage 2: dk and dv (keys outer; recomputes P from the workspace's lse and uses its D).
+ * Needs the workspace prepared by nn_fa_bwd_pre. Together with stage 3 it replaces
+ * bwd_kernel<HD>, flash_attn.cu:176-340 with its launch at :393-401 and the casts at :404. */
+int nn_fa_bwd_dkdv(const void* q, const void* k, const void* v, const void* dO,
+                   const void* workspace, size_t workspace_bytes, void* dk, void* dv,
                    int64_t B, int64_t H, int64_t KVH, int64_t T, int64_t D,
                    int dtype, float scale, void* stream);
 
-/* Backward, stage 3: scale and round the fp32 accumulators into dq, dk, dv.
- * Replaces the three `.to(kFloat16)` casts of flash_attn.cu:404. */
-int nn_fa_bwd_post(const void* workspace, size_t workspace_bytes, void* dq, void* dk, void* dv,
-                   int64_t B, int64_t H, int64_t KVH, int64_t T, int64_t D,
-                   int dtype, float scale, void* stream);
+/* Backward, stage 3: dq (queries outer). Needs the workspace prepared by nn_fa_bwd_pre. */
+int nn_fa_bwd_dq(const void* q, const void* k, const void* v, const void* dO,
+                 const void* workspace, size_t workspace_bytes, void* dq,
+                 int64_t B, int64_t H, int64_t KVH, int64_t T, int64_t D,
+                 int dtype, float scale, void* stream);
 
 /* Message of the last failed call on this thread ("" if none). Replaces the TORCH_CHECK
  * messages of flash_attn.cu:342-356 and :383-385. */

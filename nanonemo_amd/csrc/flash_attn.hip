@@ -14,11 +14,12 @@
 //     exchange with the other half-wave, and P^T feeds O^T += V^T P^T straight from registers.
 //     The running max is only moved when it grows by more than 2^8 (in base 2), so most tiles
 //     skip rescaling O; the row sum adds the 16-bit P that the product actually uses.
-//   * Backward: one block per (batch, KV head, 128-key block, chunk of query tiles). It loops
-//     over the H/KVH query heads of the group, so dK/dV of the group are summed in registers.
-//     S = Q K^T and dP = dO V^T land with the key on the lane, so P and dS feed
-//     dV^T += dO^T P and dK^T += Q^T dS as B operands; dS^T goes to LDS for dQ = dS K, which
-//     is accumulated in fp32 with atomics. dK/dV leave through LDS as coalesced fp32 atomics.
+//   * Backward in two deterministic kernels with no atomics. dK/dV: keys outer; a block owns a
+//     64-key block, its waves walk the group's query heads x query tiles, S = Q K^T and
+//     dP = dO V^T land with the key on the lane, so P and dS feed dV^T += dO^T P and
+//     dK^T += Q^T dS as B operands, and dK/dV are summed over the group's query heads in
+//     registers and LDS, then stored once. dQ: queries outer, shaped like the forward;
+//     dQ^T += K^T dS^T takes dS^T straight from registers and is stored once.
 //   * Softmax runs in base 2: exp2(s * scale * log2(e) - m'), with lse stored in natural log.
 //
 // MFMA 32x32x16 register layouts used throughout (lane l, l32 = l % 32, hh = l / 32):
@@ -120,20 +121,39 @@ __device__ inline u16x8 pack8(const f32x16& a, int base) {
 __device__ inline u16x8 cat4(u16x4 a, u16x4 b) { return __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7); }
 __device__ inline u16x8 ld8(const u16* p) { return *reinterpret_cast<const u16x8*>(p); }
 
-// Element offset of (row, col) in a row-major LDS tile of W 16-bit columns whose 16-byte chunks
-// are XOR-swizzled by the row index (spreads column reads of consecutive rows over the banks).
+// Row-major LDS tiles of W 16-bit columns store 16-byte chunk c of row r at chunk position
+// swz_chunk(r, c). The XOR pattern depends only on row bits 1..3 (W = 64) or 2..3 (W = 32), so
+// it repeats every 16 rows, and it keeps both access patterns free of bank conflicts:
+//   * ds_read_b128 of one logical chunk from 16 consecutive rows (row operands);
+//   * ds_read_b64_tr_b16 of 4 consecutive rows x 4 aligned chunks per 32 lanes (column operands).
+// It is an involution, so the DMA uses the same map to place chunks.
+template <int W>
+__device__ inline int swz_chunk(int row, int c) {
+    static_assert(W == 64 || W == 32, "tile width");
+    if constexpr (W == 64)
+        return c ^ ((((row >> 1) & 1) << 2) | ((row >> 2) & 3));
+    else
+        return c ^ ((row >> 2) & 3);
+}
 template <int W>
 __device__ inline int swz(int row, int col) {
-    constexpr int CH = W / 8;
-    return row * W + ((((col >> 3) ^ row) & (CH - 1)) << 3) + (col & 7);
+    return row * W + (swz_chunk<W>(row, col >> 3) << 3) + (col & 7);
 }
 
-// Column operand: rows r0..r0+3 of column c0 + lane%16 of a swizzled row-major tile
-// (ds_read_b64_tr_b16; r0 and c0 must be the same across each 16-lane group, c0 % 4 == 0).
+// Per-lane offset of a row operand: 8 columns col0 + 8*hh .. of row `row` (rows 16k + row read
+// the same chunk positions, so callers add 16k * W).
 template <int W>
-__device__ inline u16x4 ld_col4(const u16* tile, int r0, int c0, int lane) {
+__device__ inline int row_off(int row, int col) { return swz<W>(row, col); }
+
+// Per-lane offset of a column operand for ds_read_b64_tr_b16: lane i (of its 16-lane group)
+// addresses row r0 + i/4, columns c0 + 4*(i%4) .. +3, and receives rows r0..r0+3 of column
+// c0 + i. r0 % 4 == 0 and c0 % 16 == 0; rows 16k + r0 reuse the offset plus 16k * W.
+template <int W>
+__device__ inline int col_off(int r0, int c0, int lane) {
     const int i = lane & 15;
-    const u16* p = tile + swz<W>(r0 + (i >> 2), c0 + 4 * (i & 3));
+    return swz<W>(r0 + (i >> 2), c0 + 4 * (i & 3));
+}
+__device__ inline u16x4 ld_tr(const u16* p) {
     return __builtin_bit_cast(u16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16(LDS_AS(s16x4, const_cast<u16*>(p))));
 }
 
@@ -148,7 +168,7 @@ __device__ inline void dma_rows(const u16* __restrict__ g, int r0, int T, u16* l
         const int p0 = (it * NW + wave) * 64;  // first chunk written by this wave instruction
         const int p = p0 + lane;
         const int row = p / CH;
-        const int c = (p % CH) ^ (row & (CH - 1));
+        const int c = swz_chunk<W>(row, p % CH);
         const int gr = min(r0 + row, T - 1);
         __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(g + (size_t)gr * W + c * 8),
                                          LDS_AS(void, lds + p0 * 8), 16, 0, 0);
@@ -218,6 +238,16 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_kernel(const u16* __restrict__ 
     for (int dt = 0; dt < ND; ++dt) oacc[dt] = f32x16{};
     float m = -INFINITY, lsum = 0.f;
 
+    // Per-lane LDS offsets: K row operand (key l32 + 32t, columns 16ks + 8hh; add 32t*HD) and
+    // V^T column operand (keys 16c + 8x + 4hh.., column 32dt + l32; add 16c*HD).
+    int koff[NS], voff[ND][2];
+#pragma unroll
+    for (int ks = 0; ks < NS; ++ks) koff[ks] = row_off<HD>(l32, 16 * ks + 8 * hh);
+#pragma unroll
+    for (int dt = 0; dt < ND; ++dt)
+#pragma unroll
+        for (int x = 0; x < 2; ++x) voff[dt][x] = col_off<HD>(8 * x + 4 * hh, 32 * dt + 16 * g16, lane);
+
     const int ntiles = (min(q0 + BM, T) + BN - 1) / BN;
     auto issue = [&](int it, u16* kb, u16* vb) {
         dma_rows<HD, BN, NW>(Kp, it * BN, T, kb, wave, lane);
@@ -232,7 +262,7 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_kernel(const u16* __restrict__ 
             s[t] = f32x16{};
 #pragma unroll
             for (int ks = 0; ks < NS; ++ks)
-                s[t] = E::mfma(ld8(kb + swz<HD>(32 * t + l32, 16 * ks + 8 * hh)), qf[ks], s[t]);
+                s[t] = E::mfma(ld8(kb + 32 * t * HD + koff[ks]), qf[ks], s[t]);
         }
         // s[t][i] = score of query qrow against key k0 + 32t + (i/4)*8 + 4hh + i%4.
         if (k0 + BN - 1 > qw || k0 + BN > T) {
@@ -241,7 +271,7 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_kernel(const u16* __restrict__ 
             for (int t = 0; t < NT; ++t)
 #pragma unroll
                 for (int i = 0; i < 16; ++i)
-                    if (32 * t + (i >> 2) * 8 + (i & 3) > lim) s[t][i] = -INFINITY;
+                    s[t][i] = (32 * t + (i >> 2) * 8 + (i & 3) > lim) ? -INFINITY : s[t][i];
         }
         float mx = -INFINITY;
 #pragma unroll
@@ -274,8 +304,7 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_kernel(const u16* __restrict__ 
             // P^T chunk c holds keys 16c + (j/4)*8 + 4hh + j%4; V^T must use the same order.
 #pragma unroll
             for (int dt = 0; dt < ND; ++dt) {
-                const u16x8 va = cat4(ld_col4<HD>(vb, 16 * c + 4 * hh, 32 * dt + 16 * g16, lane),
-                                      ld_col4<HD>(vb, 16 * c + 8 + 4 * hh, 32 * dt + 16 * g16, lane));
+                const u16x8 va = cat4(ld_tr(vb + 16 * c * HD + voff[dt][0]), ld_tr(vb + 16 * c * HD + voff[dt][1]));
                 oacc[dt] = E::mfma(va, pf, oacc[dt]);
             }
         }
@@ -311,14 +340,12 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_kernel(const u16* __restrict__ 
 }
 
 // ------------------------------------------------------------------------------------------
-// Backward stage 1: D = rowsum(dO * O) and lse2 = lse * log2(e) in fp32, and zero the fp32
-// dQ/dK/dV accumulators.
+// Backward, preprocessing: D = rowsum(dO * O) and lse2 = lse * log2(e), fp32, in one pass.
 // ------------------------------------------------------------------------------------------
 template <int HD, int DT>
 __global__ __launch_bounds__(256) void fa_bwd_pre_kernel(const u16* __restrict__ O, const u16* __restrict__ dO,
                                                          const float* __restrict__ LSE, float* __restrict__ Dvec,
-                                                         float* __restrict__ Lse2, int64_t rows,
-                                                         f32x4* __restrict__ zero, int64_t nzero4) {
+                                                         float* __restrict__ Lse2, int64_t rows) {
     using E = Elem<DT>;
     constexpr int TPR = HD / 8;  // threads per row
     const int64_t gtid = (int64_t)blockIdx.x * 256 + threadIdx.x;
@@ -336,125 +363,129 @@ __global__ __launch_bounds__(256) void fa_bwd_pre_kernel(const u16* __restrict__
         Dvec[row] = acc;
         Lse2[row] = LSE[row] * kLog2e;
     }
-    const int64_t stride = (int64_t)gridDim.x * 256;
-    for (int64_t i = gtid; i < nzero4; i += stride) zero[i] = f32x4{};
 }
 
 // ------------------------------------------------------------------------------------------
-// Backward stage 2. Block = 4 waves = 128 keys of one (batch, KV head); wave w owns keys
-// kb0 + 32w .. +31 and keeps K, V (B operands) and its dK^T, dV^T accumulators in registers.
-// The block walks the group's query heads x a chunk of 64-row query tiles; per tile:
-//   S = Q K^T, dP = dO V^T             (A = Q / dO rows, LDS; B = K / V, registers)
+// Backward, dK / dV. Block = 8 waves = 4 groups of 2 waves. A group's two waves own 32 keys
+// each of a 64-key block ("unit") and keep K, V (B operands) and their dK^T, dV^T accumulators
+// in registers. The 4 groups split the unit's (query head, 64-row query tile) iterations
+// round-robin, each streaming its own Q / dO tiles through LDS by DMA, so every KV head's
+// gradient is summed over its H/KVH query heads without repeating K or V. At the end of a unit
+// the 4 partial dK / dV are summed through LDS and stored once in the output dtype (no atomics,
+// no fp32 round trip through HBM). A block takes unit j and unit nkb-1-j, so every block
+// carries the same causal work. Per tile:
+//   S = Q K^T, dP = dO V^T             (A = Q / dO rows from LDS, B = K / V registers)
 //   P = exp2(S*sl2 - lse2), dS = P (dP - D)
-//   dV^T += dO^T P, dK^T += Q^T dS     (A = columns of the Q / dO tiles; B = P / dS registers)
-//   dQ += dS K                         (A = columns of dS^T in LDS, B = columns of K in LDS)
-// Q/dO tiles of the next iteration stream in by DMA while the current one is computed, and each
-// tile's dQ partial is added to the fp32 accumulator with atomics. The softmax scale is folded
-// into the final dQ/dK conversion (stage 3).
+//   dV^T += dO^T P, dK^T += Q^T dS     (A = columns of the Q / dO tiles, B = P / dS registers)
 // ------------------------------------------------------------------------------------------
 template <int HD, int DT>
-__global__ __launch_bounds__(256, 2) void fa_bwd_main_kernel(
+__global__ __launch_bounds__(512, 1) void fa_bwd_dkdv_kernel(
     const u16* __restrict__ Q, const u16* __restrict__ K, const u16* __restrict__ V, const u16* __restrict__ dO,
-    const float* __restrict__ Lse2, const float* __restrict__ Dvec, float* __restrict__ dQa, float* __restrict__ dKa,
-    float* __restrict__ dVa, int BKV, int H, int KVH, int T, int nkb, int nqt, int qchunk, float sl2) {
+    const float* __restrict__ Lse2, const float* __restrict__ Dvec, u16* __restrict__ dK, u16* __restrict__ dV,
+    int BKV, int H, int KVH, int T, int nkb, int nqt, float sl2, float scale) {
     using E = Elem<DT>;
-    constexpr int BN = 128, BM = 64, NW = 4;
+    constexpr int BNK = 64, BM = 64, NG = 4, GW = 2;
     constexpr int NS = HD / 16;
     constexpr int ND = HD / 32;
     constexpr int QT = BM * HD;  // elements of one Q or dO tile
-    __shared__ __attribute__((aligned(16))) u16 qA[QT];
-    __shared__ __attribute__((aligned(16))) u16 oA[QT];
-    __shared__ __attribute__((aligned(16))) u16 qB[QT];
-    __shared__ __attribute__((aligned(16))) u16 oB[QT];
-    __shared__ __attribute__((aligned(16))) u16 kS[BN * HD];   // K rows of the block (dQ's B operand)
-    __shared__ __attribute__((aligned(16))) u16 dsT[BN * BM];  // dS^T [key][query]
-    __shared__ __attribute__((aligned(16))) float lA[2 * BM];  // lse2 | D of the tile in qA/oA
-    __shared__ __attribute__((aligned(16))) float lB[2 * BM];
+    constexpr int CH4 = HD / 4;  // 16-byte fp32 chunks per staged gradient row
+    static_assert(BNK == BM, "a unit's first query tile is its own index");
+    __shared__ __attribute__((aligned(16))) u16 qA[NG * QT];
+    __shared__ __attribute__((aligned(16))) u16 oA[NG * QT];
+    __shared__ __attribute__((aligned(16))) u16 qB[NG * QT];
+    __shared__ __attribute__((aligned(16))) u16 oB[NG * QT];
+    __shared__ __attribute__((aligned(16))) float lA[NG * 2 * BM];  // per group: lse2 | D
+    __shared__ __attribute__((aligned(16))) float lB[NG * 2 * BM];
 
     const int bid = blockIdx.x;
     const int bk = bid % BKV;
-    const int item = bid / BKV;
-    const int c = item / nkb, j = item - (item / nkb) * nkb;
-    const int qt_first = (j * BN) / BM;
-    const int qt_hi = nqt - c * qchunk;
-    if (qt_hi <= qt_first) return;  // this (key block, chunk) pair has no work
-    const int qt_lo = max(qt_first, qt_hi - qchunk);
-    const int nq = qt_hi - qt_lo;
-
+    const int pj = bid / BKV;
     const int b = bk / KVH, kvh = bk - b * KVH, group = H / KVH;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
     const int g16 = (lane >> 4) & 1;
-    const int kb0 = j * BN, kw = kb0 + 32 * wave, key = kw + l32;
+    const int gi = wave >> 1, wk = wave & 1, gtid = tid & (64 * GW - 1);
     const size_t kvoff = (size_t)bk * T * HD;
 
-    u16x8 kf[NS], vf[NS];
+    int qroff[NS], qcoff[ND][2];
 #pragma unroll
-    for (int s = 0; s < NS; ++s) {
-        kf[s] = key < T ? ld8(K + kvoff + (size_t)key * HD + 16 * s + 8 * hh) : u16x8{};
-        vf[s] = key < T ? ld8(V + kvoff + (size_t)key * HD + 16 * s + 8 * hh) : u16x8{};
-    }
-    dma_rows<HD, BN, NW>(K + kvoff, kb0, T, kS, wave, lane);
-
-    f32x16 dk[ND], dv[ND];
+    for (int ks = 0; ks < NS; ++ks) qroff[ks] = row_off<HD>(l32, 16 * ks + 8 * hh);
 #pragma unroll
-    for (int dt = 0; dt < ND; ++dt) dk[dt] = dv[dt] = f32x16{};
+    for (int dt = 0; dt < ND; ++dt)
+#pragma unroll
+        for (int x = 0; x < 2; ++x) qcoff[dt][x] = col_off<HD>(8 * x + 4 * hh, 32 * dt + 16 * g16, lane);
 
-    // dQ tile of this wave: query rows 32*dq_qh.., head_dim columns 32*dq_dt.. of the 64 x HD tile.
-    const bool dq_wave = wave < 2 * ND;
-    const int dq_qh = wave / ND, dq_dt = wave - (wave / ND) * ND;
+    for (int ui = 0; ui < 2; ++ui) {
+        const int unit = ui == 0 ? pj : nkb - 1 - pj;
+        if (ui == 1 && unit <= pj) break;  // an odd unit count leaves the middle unit alone
+        const int kb0 = unit * BNK, kw = kb0 + 32 * wk, key = kw + l32;
+        const int qt_first = unit, nq = nqt - qt_first, niter = group * nq;
+        const int rounds = (niter + NG - 1) / NG;
 
-    const int niter = group * nq;
-    float lse_r = 0.f, d_r = 0.f;
-    auto issue = [&](int itn, u16* qb_, u16* ob_) {
-        const int g = itn / nq, qt = qt_lo + itn - g * nq;
-        const int hq = kvh * group + g;
-        const size_t qoff = ((size_t)b * H + hq) * T * HD;
-        dma_rows<HD, BM, NW>(Q + qoff, qt * BM, T, qb_, wave, lane);
-        dma_rows<HD, BM, NW>(dO + qoff, qt * BM, T, ob_, wave, lane);
-        if (tid < 2 * BM) {
-            const int q = min(qt * BM + (tid & (BM - 1)), T - 1);
-            const size_t ro = ((size_t)b * H + hq) * T + q;
-            if (tid < BM) lse_r = Lse2[ro];
-            else d_r = Dvec[ro];
+        u16x8 kf[NS], vf[NS];
+#pragma unroll
+        for (int s = 0; s < NS; ++s) {
+            kf[s] = key < T ? ld8(K + kvoff + (size_t)key * HD + 16 * s + 8 * hh) : u16x8{};
+            vf[s] = key < T ? ld8(V + kvoff + (size_t)key * HD + 16 * s + 8 * hh) : u16x8{};
         }
-    };
-    // One query tile. On entry the tile's Q / dO rows (qb_, ob_) and lse2 / D (lb_) are in LDS
-    // for this wave; the next tile is fetched into (qn_, on_, ln_) while this one is computed.
-    auto step = [&](int itn, const u16* qb_, const u16* ob_, const float* lb_, u16* qn_, u16* on_, float* ln_) {
-        const int g = itn / nq, qt = qt_lo + itn - g * nq;
-        const int hq = kvh * group + g;
-        const int qbase = qt * BM;
-        __syncthreads();
-        const bool more = itn + 1 < niter;
-        if (more) issue(itn + 1, qn_, on_);
+        f32x16 dk[ND], dv[ND];
+#pragma unroll
+        for (int dt = 0; dt < ND; ++dt) dk[dt] = dv[dt] = f32x16{};
 
-        if (kw <= qbase + BM - 1 && kw < T) {
+        float lse_r = 0.f, d_r = 0.f;
+        // Fetch iteration itn's Q / dO rows into this group's slot (the group's two waves DMA).
+        auto issue = [&](int itn, u16* qs, u16* os) {
+            const int g = itn / nq, qt = qt_first + itn - g * nq;
+            const int hq = kvh * group + g;
+            const size_t qoff = ((size_t)b * H + hq) * T * HD;
+            dma_rows<HD, BM, GW>(Q + qoff, qt * BM, T, qs + gi * QT, wk, lane);
+            dma_rows<HD, BM, GW>(dO + qoff, qt * BM, T, os + gi * QT, wk, lane);
+            const int q = min(qt * BM + (gtid & (BM - 1)), T - 1);
+            const size_t ro = ((size_t)b * H + hq) * T + q;
+            if (gtid < BM) lse_r = Lse2[ro];
+            else d_r = Dvec[ro];
+        };
+        auto compute = [&](int itn, const u16* qs, const u16* os, const float* ls) {
+            const int g = itn / nq, qt = qt_first + itn - g * nq;
+            const int qbase = qt * BM;
+            if (kw > qbase + BM - 1 || kw >= T) return;  // every key of this wave is in the future
+            const u16* qb_ = qs + gi * QT;
+            const u16* ob_ = os + gi * QT;
+            const float* lb_ = ls + gi * 2 * BM;
             const bool need_mask = (kw + 31 > qbase) || (qbase + BM > T) || (kw + 32 > T);
             const int qlim = key - qbase - 4 * hh;  // query offsets below this are in the future of the key
-            // One 32-query half at a time keeps S, dP and their 16-bit forms for 32 queries live.
 #pragma unroll 1
             for (int qh = 0; qh < 2; ++qh) {
                 f32x16 s = f32x16{}, dp = f32x16{};
+                const u16* qrow = qb_ + 32 * qh * HD;
+                const u16* orow = ob_ + 32 * qh * HD;
 #pragma unroll
                 for (int ks = 0; ks < NS; ++ks) {
-                    s = E::mfma(ld8(qb_ + swz<HD>(32 * qh + l32, 16 * ks + 8 * hh)), kf[ks], s);
-                    dp = E::mfma(ld8(ob_ + swz<HD>(32 * qh + l32, 16 * ks + 8 * hh)), vf[ks], dp);
+                    s = E::mfma(ld8(qrow + qroff[ks]), kf[ks], s);
+                    dp = E::mfma(ld8(orow + qroff[ks]), vf[ks], dp);
                 }
                 // s[i]: query qbase + 32qh + (i/4)*8 + 4hh + i%4 against this lane's key.
+                const float* lq = lb_ + 32 * qh + 4 * hh;
 #pragma unroll
                 for (int g4 = 0; g4 < 4; ++g4) {
-                    const int ql = 32 * qh + 8 * g4 + 4 * hh;
-                    const f32x4 L = *reinterpret_cast<const f32x4*>(&lb_[ql]);
-                    const f32x4 Dd = *reinterpret_cast<const f32x4*>(&lb_[BM + ql]);
+                    const f32x4 L = *reinterpret_cast<const f32x4*>(lq + 8 * g4);
+                    const f32x4 Dd = *reinterpret_cast<const f32x4*>(lq + BM + 8 * g4);
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
                         const int i = 4 * g4 + r;
-                        float p = fast_exp2(fmaf(s[i], sl2, -L[r]));
-                        float ds = p * (dp[i] - Dd[r]);
-                        // visible iff key <= q, q < T and key < T
-                        if (need_mask && (32 * qh + 8 * g4 + r < qlim || qbase + ql + r >= T || key >= T)) p = ds = 0.f;
+                        const float p = fast_exp2(fmaf(s[i], sl2, -L[r]));
+                        dp[i] = p * (dp[i] - Dd[r]);
                         s[i] = p;
-                        dp[i] = ds;
+                    }
+                }
+                if (need_mask) {  // visible iff key <= q, q < T and key < T
+                    const int qrem = T - qbase - 32 * qh - 4 * hh;  // query offsets >= this are past T
+                    const bool kin = key < T;
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) {
+                        const int qo = 32 * qh + (i >> 2) * 8 + (i & 3);
+                        const bool keep = (qo >= qlim) & ((i >> 2) * 8 + (i & 3) < qrem) & kin;
+                        s[i] = keep ? s[i] : 0.f;
+                        dp[i] = keep ? dp[i] : 0.f;
                     }
                 }
 #pragma unroll
@@ -462,117 +493,199 @@ __global__ __launch_bounds__(256, 2) void fa_bwd_main_kernel(
                     const int qc = 2 * qh + half;  // 16-query chunk: queries 16qc + (j/4)*8 + 4hh + j%4
                     const u16x8 pf = pack8<DT>(s, 8 * half);
                     const u16x8 sf = pack8<DT>(dp, 8 * half);
+                    const u16* ocol = ob_ + 16 * qc * HD;
+                    const u16* qcol = qb_ + 16 * qc * HD;
 #pragma unroll
                     for (int dt = 0; dt < ND; ++dt) {
-                        const int c0 = 32 * dt + 16 * g16;
-                        const u16x8 ga = cat4(ld_col4<HD>(ob_, 16 * qc + 4 * hh, c0, lane),
-                                              ld_col4<HD>(ob_, 16 * qc + 8 + 4 * hh, c0, lane));
-                        dv[dt] = E::mfma(ga, pf, dv[dt]);
-                        const u16x8 qa = cat4(ld_col4<HD>(qb_, 16 * qc + 4 * hh, c0, lane),
-                                              ld_col4<HD>(qb_, 16 * qc + 8 + 4 * hh, c0, lane));
-                        dk[dt] = E::mfma(qa, sf, dk[dt]);
+                        dv[dt] = E::mfma(cat4(ld_tr(ocol + qcoff[dt][0]), ld_tr(ocol + qcoff[dt][1])), pf, dv[dt]);
+                        dk[dt] = E::mfma(cat4(ld_tr(qcol + qcoff[dt][0]), ld_tr(qcol + qcoff[dt][1])), sf, dk[dt]);
                     }
-                    // dS^T row (this lane's key): 4 consecutive queries per 8-byte store.
-                    const u32x4 w = __builtin_bit_cast(u32x4, sf);
-                    const int qa0 = 16 * qc + 4 * hh;
-                    *reinterpret_cast<u32x2*>(dsT + swz<BM>(32 * wave + l32, qa0)) = u32x2{w[0], w[1]};
-                    *reinterpret_cast<u32x2*>(dsT + swz<BM>(32 * wave + l32, qa0 + 8)) = u32x2{w[2], w[3]};
                 }
             }
-        }
-        __syncthreads();
-
-        // dQ tile over the keys that can be visible (every other dS^T row is never read).
-        int kvis = min(BN, qbase + BM - kb0);
-        kvis = min(kvis, T - kb0);
-        const int nks = (kvis + 15) / 16;
-        f32x16 dqacc = f32x16{};
-        if (dq_wave) {
-            const int cq = 32 * dq_qh + 16 * g16, cd = 32 * dq_dt + 16 * g16;
-            for (int ks = 0; ks < nks; ++ks) {
-                const u16x8 a = cat4(ld_col4<BM>(dsT, 16 * ks + 8 * hh, cq, lane),
-                                     ld_col4<BM>(dsT, 16 * ks + 8 * hh + 4, cq, lane));
-                const u16x8 bb = cat4(ld_col4<HD>(kS, 16 * ks + 8 * hh, cd, lane),
-                                      ld_col4<HD>(kS, 16 * ks + 8 * hh + 4, cd, lane));
-                dqacc = E::mfma(a, bb, dqacc);
-            }
-        }
-        // The next tile's DMA and lse2 / D loads (and the previous dQ atomics) are done after this.
-        wait_vmem();
-        if (more && tid < 2 * BM) ln_[tid] = tid < BM ? lse_r : d_r;
-        if (dq_wave) {
-            float* dst = dQa + (((size_t)b * H + hq) * T + qbase) * HD + 32 * dq_dt + l32;
-            const int rows = min(BM, T - qbase);
-#pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                const int r = 32 * dq_qh + (i >> 2) * 8 + 4 * hh + (i & 3);
-                if (r < rows) unsafeAtomicAdd(dst + (size_t)r * HD, dqacc[i]);
-            }
-        }
-    };
-
-    issue(0, qA, oA);
-    wait_vmem();
-    if (tid < 2 * BM) lA[tid] = tid < BM ? lse_r : d_r;
-    for (int itn = 0; itn < niter; itn += 2) {
-        step(itn, qA, oA, lA, qB, oB, lB);
-        if (itn + 1 >= niter) break;
-        step(itn + 1, qB, oB, lB, qA, oA, lA);
-    }
-
-    // dK^T / dV^T accumulators (lane = key, element i = column 32dt + (i/4)*8 + 4hh + i%4) leave
-    // through LDS so that each atomic instruction covers 64 consecutive floats of one tensor.
-    float* stage = reinterpret_cast<float*>(dsT);  // 128 keys x 32 columns fp32 = the dS^T tile's bytes
-    static_assert(BN * 32 * 4 == BN * BM * 2, "staging must fit the dS^T tile");
-#pragma unroll
-    for (int which = 0; which < 2; ++which)
-#pragma unroll
-        for (int dt = 0; dt < ND; ++dt) {
+        };
+        // Round r: group gi computes iteration NG*r + gi while fetching NG*(r+1) + gi.
+        auto round = [&](int r, const u16* qs, const u16* os, const float* ls, u16* qn, u16* on, float* ln) {
+            const int itn = NG * r + gi, nxt = itn + NG;
             __syncthreads();
-            const f32x16& a = which == 0 ? dk[dt] : dv[dt];
-            const int r = 32 * wave + l32;
+            if (nxt < niter) issue(nxt, qn, on);
+            if (itn < niter) compute(itn, qs, os, ls);
+            wait_vmem();
+            if (nxt < niter) ln[gi * 2 * BM + gtid] = gtid < BM ? lse_r : d_r;
+        };
+
+        if (gi < niter) issue(gi, qA, oA);
+        wait_vmem();
+        if (gi < niter) lA[gi * 2 * BM + gtid] = gtid < BM ? lse_r : d_r;
+        for (int r = 0; r < rounds; r += 2) {
+            round(r, qA, oA, lA, qB, oB, lB);
+            if (r + 1 >= rounds) break;
+            round(r + 1, qB, oB, lB, qA, oA, lA);
+        }
+
+        // Sum the groups' partial dK^T / dV^T (lane = key, element i = column
+        // 32dt + (i/4)*8 + 4hh + i%4) through LDS: [64 keys][HD] fp32 per (tensor, group), 16-byte
+        // chunks XOR-swizzled by row.
+        __syncthreads();
+        float* sk = reinterpret_cast<float*>(gi < 2 ? qA : oA) + (gi & 1) * BNK * HD;
+        float* sv = reinterpret_cast<float*>(gi < 2 ? qB : oB) + (gi & 1) * BNK * HD;
+        const int kr = 32 * wk + l32;
+#pragma unroll
+        for (int dt = 0; dt < ND; ++dt)
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
-                const int col = 8 * g + 4 * hh;  // 4 consecutive columns
-                *reinterpret_cast<f32x4*>(stage + r * 32 + (((col >> 2) ^ (r & 7)) << 2)) =
-                    f32x4{a[4 * g], a[4 * g + 1], a[4 * g + 2], a[4 * g + 3]};
+                const int cc = ((8 * dt + 2 * g + hh) ^ kr) & (CH4 - 1);
+                *reinterpret_cast<f32x4*>(sk + kr * HD + 4 * cc) = f32x4{dk[dt][4 * g], dk[dt][4 * g + 1], dk[dt][4 * g + 2], dk[dt][4 * g + 3]};
+                *reinterpret_cast<f32x4*>(sv + kr * HD + 4 * cc) = f32x4{dv[dt][4 * g], dv[dt][4 * g + 1], dv[dt][4 * g + 2], dv[dt][4 * g + 3]};
             }
-            __syncthreads();
-            float* dst = (which == 0 ? dKa : dVa) + kvoff + 32 * dt;
+        __syncthreads();
 #pragma unroll
-            for (int k = 0; k < BN * 32 / 256; ++k) {
-                const int f = tid + 256 * k;
-                const int row = f >> 5, col = f & 31;
-                if (kb0 + row < T)
-                    unsafeAtomicAdd(dst + (size_t)(kb0 + row) * HD + col,
-                                    stage[row * 32 + ((((col >> 2) ^ (row & 7)) << 2) | (col & 3))]);
+        for (int k = 0; k < 2 * BNK * CH4 / 512; ++k) {
+            const int it = tid + 512 * k;
+            const int which = it / (BNK * CH4), rem = it - which * (BNK * CH4);
+            const int row = rem / CH4, c = rem - row * CH4;
+            const int off = row * HD + 4 * ((c ^ row) & (CH4 - 1));
+            const float* s0 = which == 0 ? reinterpret_cast<const float*>(qA) : reinterpret_cast<const float*>(qB);
+            const float* s1 = which == 0 ? reinterpret_cast<const float*>(oA) : reinterpret_cast<const float*>(oB);
+            f32x4 acc = *reinterpret_cast<const f32x4*>(s0 + off);
+            acc += *reinterpret_cast<const f32x4*>(s0 + BNK * HD + off);
+            acc += *reinterpret_cast<const f32x4*>(s1 + off);
+            acc += *reinterpret_cast<const f32x4*>(s1 + BNK * HD + off);
+            if (which == 0) acc *= scale;
+            if (kb0 + row < T) {
+                u16* dst = (which == 0 ? dK : dV) + kvoff + (size_t)(kb0 + row) * HD + 4 * c;
+                *reinterpret_cast<u32x2*>(dst) = u32x2{E::pack2(acc[0], acc[1]), E::pack2(acc[2], acc[3])};
             }
         }
+        __syncthreads();  // the staging area is the next unit's tile space
+    }
 }
 
 // ------------------------------------------------------------------------------------------
-// Backward stage 3: dq = dQacc * scale, dk = dKacc * scale, dv = dVacc, rounded to 16 bits.
+// Backward, dQ. Shaped like the forward: block = 4 waves = 128 query rows of one (batch, head),
+// 64-key tiles of K and V double-buffered in LDS by DMA, Q and dO rows in registers, lse2 and D
+// per lane. Per tile:
+//   S^T = K Q^T, dP^T = V dO^T          (A = K / V rows from LDS, B = Q / dO registers)
+//   dS^T = exp2(S^T*sl2 - lse2) (dP^T - D)
+//   dQ^T += K^T dS^T                    (A = columns of the K tile, B = dS^T registers)
+// dQ stays in registers for the whole key loop and is stored once, scaled, in the output dtype.
 // ------------------------------------------------------------------------------------------
-template <int DT>
-__global__ __launch_bounds__(256) void fa_bwd_post_kernel(const f32x4* __restrict__ dQa, const f32x4* __restrict__ dKa,
-                                                          const f32x4* __restrict__ dVa, u32x2* __restrict__ dq,
-                                                          u32x2* __restrict__ dk, u32x2* __restrict__ dv, int64_t nq4,
-                                                          int64_t nk4, float scale) {
+template <int HD, int DT>
+__global__ __launch_bounds__(256, 2) void fa_bwd_dq_kernel(const u16* __restrict__ Q, const u16* __restrict__ K,
+                                                           const u16* __restrict__ V, const u16* __restrict__ dO,
+                                                           const float* __restrict__ Lse2,
+                                                           const float* __restrict__ Dvec, u16* __restrict__ dQ, int BH,
+                                                           int H, int KVH, int T, int nqb, float sl2, float scale) {
     using E = Elem<DT>;
-    const int64_t stride = (int64_t)gridDim.x * 256;
-    const int64_t total = nq4 + 2 * nk4;
-    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += stride) {
-        f32x4 x;
-        float s;
-        u32x2* dst;
-        if (i < nq4) {
-            x = dQa[i], s = scale, dst = dq + i;
-        } else if (i < nq4 + nk4) {
-            x = dKa[i - nq4], s = scale, dst = dk + (i - nq4);
-        } else {
-            x = dVa[i - nq4 - nk4], s = 1.f, dst = dv + (i - nq4 - nk4);
+    constexpr int BM = 128, BN = 64, NW = 4;
+    constexpr int NS = HD / 16;
+    constexpr int ND = HD / 32;
+    constexpr int NT = BN / 32;
+    constexpr int TILE = BN * HD;
+    __shared__ __attribute__((aligned(16))) u16 kA[TILE];
+    __shared__ __attribute__((aligned(16))) u16 vA[TILE];
+    __shared__ __attribute__((aligned(16))) u16 kB[TILE];
+    __shared__ __attribute__((aligned(16))) u16 vB[TILE];
+
+    const int bid = blockIdx.x;
+    const int bh = bid % BH;
+    const int qb = nqb - 1 - bid / BH;
+    const int b = bh / H, h = bh - b * H;
+    const int kvh = h / (H / KVH);
+    const size_t qoff = (size_t)bh * T * HD;
+    const size_t kvoff = ((size_t)b * KVH + kvh) * T * HD;
+    const u16* Kp = K + kvoff;
+    const u16* Vp = V + kvoff;
+
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
+    const int g16 = (lane >> 4) & 1;
+    const int q0 = qb * BM, qw = q0 + wave * 32, qrow = qw + l32;
+    const int qc_ = min(qrow, T - 1);
+
+    u16x8 qf[NS], gf[NS];
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+        qf[s] = ld8(Q + qoff + (size_t)qc_ * HD + 16 * s + 8 * hh);
+        gf[s] = ld8(dO + qoff + (size_t)qc_ * HD + 16 * s + 8 * hh);
+    }
+    const float lse2 = Lse2[(size_t)bh * T + qc_];
+    const float dd = Dvec[(size_t)bh * T + qc_];
+
+    int koff[NS], kcol[ND][2];
+#pragma unroll
+    for (int ks = 0; ks < NS; ++ks) koff[ks] = row_off<HD>(l32, 16 * ks + 8 * hh);
+#pragma unroll
+    for (int dt = 0; dt < ND; ++dt)
+#pragma unroll
+        for (int x = 0; x < 2; ++x) kcol[dt][x] = col_off<HD>(8 * x + 4 * hh, 32 * dt + 16 * g16, lane);
+
+    f32x16 dq[ND];
+#pragma unroll
+    for (int dt = 0; dt < ND; ++dt) dq[dt] = f32x16{};
+
+    const int ntiles = (min(q0 + BM, T) + BN - 1) / BN;
+    auto issue = [&](int it, u16* kb, u16* vb) {
+        dma_rows<HD, BN, NW>(Kp, it * BN, T, kb, wave, lane);
+        dma_rows<HD, BN, NW>(Vp, it * BN, T, vb, wave, lane);
+    };
+    auto step = [&](int it, const u16* kb, const u16* vb) {
+        const int k0 = it * BN;
+        if (qw >= T || k0 > qw + 31) return;  // no visible key in this tile for this wave
+        f32x16 s[NT], dp[NT];
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            s[t] = f32x16{};
+            dp[t] = f32x16{};
+#pragma unroll
+            for (int ks = 0; ks < NS; ++ks) {
+                s[t] = E::mfma(ld8(kb + 32 * t * HD + koff[ks]), qf[ks], s[t]);
+                dp[t] = E::mfma(ld8(vb + 32 * t * HD + koff[ks]), gf[ks], dp[t]);
+            }
         }
-        *dst = u32x2{E::pack2(x[0] * s, x[1] * s), E::pack2(x[2] * s, x[3] * s)};
+        // s[t][i]: key k0 + 32t + (i/4)*8 + 4hh + i%4 against query qrow.
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) dp[t][i] = fast_exp2(fmaf(s[t][i], sl2, -lse2)) * (dp[t][i] - dd);
+        if (k0 + BN - 1 > qw || k0 + BN > T) {
+            const int lim = min(qrow, T - 1) - k0 - 4 * hh;
+#pragma unroll
+            for (int t = 0; t < NT; ++t)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) dp[t][i] = (32 * t + (i >> 2) * 8 + (i & 3) > lim) ? 0.f : dp[t][i];
+        }
+#pragma unroll
+        for (int c = 0; c < BN / 16; ++c) {
+            const u16x8 sf = pack8<DT>(dp[c >> 1], 8 * (c & 1));  // keys 16c + (j/4)*8 + 4hh + j%4
+            const u16* kc = kb + 16 * c * HD;
+#pragma unroll
+            for (int dt = 0; dt < ND; ++dt)
+                dq[dt] = E::mfma(cat4(ld_tr(kc + kcol[dt][0]), ld_tr(kc + kcol[dt][1])), sf, dq[dt]);
+        }
+    };
+
+    issue(0, kA, vA);
+    for (int it = 0; it < ntiles; it += 2) {
+        wait_vmem();
+        __syncthreads();
+        if (it + 1 < ntiles) issue(it + 1, kB, vB);
+        step(it, kA, vA);
+        if (it + 1 >= ntiles) break;
+        wait_vmem();
+        __syncthreads();
+        if (it + 2 < ntiles) issue(it + 2, kA, vA);
+        step(it + 1, kB, vB);
+    }
+
+    if (qrow < T) {
+        u16* dst = dQ + qoff + (size_t)qrow * HD;
+#pragma unroll
+        for (int dt = 0; dt < ND; ++dt)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const f32x16& a = dq[dt];
+                u32x2 w = {E::pack2(a[4 * g] * scale, a[4 * g + 1] * scale), E::pack2(a[4 * g + 2] * scale, a[4 * g + 3] * scale)};
+                *reinterpret_cast<u32x2*>(dst + 32 * dt + 8 * g + 4 * hh) = w;
+            }
     }
 }
 
@@ -601,8 +714,9 @@ int launch_status(const char* what) {
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
 int check_dims(int64_t B, int64_t H, int64_t KVH, int64_t T, int64_t D, int dtype) {
-    if (B < 0 || H <= 0 || KVH <= 0 || T < 0) return fail(-1, "invalid sizes B=%lld H=%lld KVH=%lld T=%lld",
-                                                          (long long)B, (long long)H, (long long)KVH, (long long)T);
+    if (B < 0 || H <= 0 || KVH <= 0 || T < 0)
+        return fail(-1, "invalid sizes B=%lld H=%lld KVH=%lld T=%lld", (long long)B, (long long)H, (long long)KVH,
+                    (long long)T);
     if (D != 32 && D != 64) return fail(-1, "head_dim must be 32 or 64");
     if (H % KVH != 0) return fail(-1, "query heads must group evenly over KV heads");
     if (dtype != kF16 && dtype != kBF16) return fail(-1, "inputs must be float16 or bfloat16");
@@ -611,10 +725,8 @@ int check_dims(int64_t B, int64_t H, int64_t KVH, int64_t T, int64_t D, int dtyp
     return 0;
 }
 
+// Backward workspace: D = rowsum(dO * o) and lse * log2(e), one fp32 per query row each.
 struct Workspace {
-    float* dq;
-    float* dk;
-    float* dv;
     float* D;
     float* lse2;
     size_t bytes;
@@ -622,25 +734,13 @@ struct Workspace {
 
 size_t round256(size_t n) { return (n + 255) & ~(size_t)255; }
 
-Workspace carve(void* base, int64_t B, int64_t H, int64_t KVH, int64_t T, int64_t D) {
-    const size_t nq = (size_t)B * H * T * D, nk = (size_t)B * KVH * T * D, nr = (size_t)B * H * T;
-    char* p = (char*)base;
+Workspace carve(void* base, int64_t B, int64_t H, int64_t T) {
+    const size_t vec = round256(4 * (size_t)B * H * T);
     Workspace w;
-    w.dq = (float*)p;
-    w.dk = w.dq + nq;  // dQ, dK, dV accumulators are adjacent so one pass can zero them
-    w.dv = w.dk + nk;
-    const size_t acc = round256(4 * (nq + 2 * nk)), vec = round256(4 * nr);
-    w.D = (float*)(p + acc);
-    w.lse2 = (float*)(p + acc + vec);
-    w.bytes = acc + 2 * vec;
+    w.D = (float*)base;
+    w.lse2 = (float*)((char*)base + vec);
+    w.bytes = 2 * vec;
     return w;
-}
-
-int env_int(const char* name, int dflt) {
-    const char* s = getenv(name);
-    if (!s || !*s) return dflt;
-    const int v = atoi(s);
-    return v > 0 ? v : dflt;
 }
 
 template <int HD, int DT>
@@ -656,46 +756,49 @@ int fwd_impl(const void* q, const void* k, const void* v, void* o, float* lse, i
 template <int HD, int DT>
 int pre_impl(const void* o, const void* dO, const float* lse, const Workspace& w, int64_t B, int64_t H, int64_t KVH,
              int64_t T, hipStream_t st) {
+    (void)KVH;
     const int64_t rows = B * H * T;
-    const int64_t threads = rows * (HD / 8);
-    const int64_t nzero4 = (B * H * T * HD + 2 * B * KVH * T * HD) / 4;
-    int64_t blocks = (threads + 255) / 256;
-    if (blocks < 1) blocks = 1;
+    const int64_t blocks = (rows * (HD / 8) + 255) / 256;
     fa_bwd_pre_kernel<HD, DT><<<dim3((unsigned)blocks), dim3(256), 0, st>>>((const u16*)o, (const u16*)dO, lse, w.D,
-                                                                           w.lse2, rows, (f32x4*)w.dq, nzero4);
+                                                                           w.lse2, rows);
     return launch_status("fa_bwd_pre_kernel");
 }
 
 template <int HD, int DT>
-int main_impl(const void* q, const void* k, const void* v, const void* dO, const Workspace& w, int64_t B, int64_t H,
-              int64_t KVH, int64_t T, float scale, hipStream_t st) {
-    const int nkb = (int)((T + 127) / 128);
-    const int nqt = (int)((T + 63) / 64);
-    static const int qchunk = env_int("NNFA_BWD_QCHUNK", 4);
-    const int nch = (nqt + qchunk - 1) / qchunk;
+int dkdv_impl(const void* q, const void* k, const void* v, const void* dO, const Workspace& w, void* dk, void* dv,
+              int64_t B, int64_t H, int64_t KVH, int64_t T, float scale, hipStream_t st) {
+    const int nkb = (int)((T + 63) / 64);  // 64-key units
+    const int nqt = nkb;                   // 64-row query tiles
+    const int npairs = (nkb + 1) / 2;
     const int BKV = (int)(B * KVH);
-    fa_bwd_main_kernel<HD, DT><<<dim3(nch * nkb * BKV), dim3(256), 0, st>>>(
-        (const u16*)q, (const u16*)k, (const u16*)v, (const u16*)dO, w.lse2, w.D, w.dq, w.dk, w.dv, BKV, (int)H,
-        (int)KVH, (int)T, nkb, nqt, qchunk, scale * kLog2e);
-    return launch_status("fa_bwd_main_kernel");
+    fa_bwd_dkdv_kernel<HD, DT><<<dim3(npairs * BKV), dim3(512), 0, st>>>(
+        (const u16*)q, (const u16*)k, (const u16*)v, (const u16*)dO, w.lse2, w.D, (u16*)dk, (u16*)dv, BKV, (int)H,
+        (int)KVH, (int)T, nkb, nqt, scale * kLog2e, scale);
+    return launch_status("fa_bwd_dkdv_kernel");
 }
 
-template <int DT>
-int post_impl(const Workspace& w, void* dq, void* dk, void* dv, int64_t B, int64_t H, int64_t KVH, int64_t T,
-              int64_t D, float scale, hipStream_t st) {
-    const int64_t nq4 = B * H * T * D / 4, nk4 = B * KVH * T * D / 4;
-    int64_t blocks = (nq4 + 2 * nk4 + 255) / 256;
-    if (blocks > 8192) blocks = 8192;
-    if (blocks < 1) blocks = 1;
-    fa_bwd_post_kernel<DT><<<dim3((unsigned)blocks), dim3(256), 0, st>>>(
-        (const f32x4*)w.dq, (const f32x4*)w.dk, (const f32x4*)w.dv, (u32x2*)dq, (u32x2*)dk, (u32x2*)dv, nq4, nk4,
-        scale);
-    return launch_status("fa_bwd_post_kernel");
+template <int HD, int DT>
+int dq_impl(const void* q, const void* k, const void* v, const void* dO, const Workspace& w, void* dq, int64_t B,
+            int64_t H, int64_t KVH, int64_t T, float scale, hipStream_t st) {
+    const int nqb = (int)((T + 127) / 128);
+    const int BH = (int)(B * H);
+    fa_bwd_dq_kernel<HD, DT><<<dim3(nqb * BH), dim3(256), 0, st>>>(
+        (const u16*)q, (const u16*)k, (const u16*)v, (const u16*)dO, w.lse2, w.D, (u16*)dq, BH, (int)H, (int)KVH,
+        (int)T, nqb, scale * kLog2e, scale);
+    return launch_status("fa_bwd_dq_kernel");
+}
+
+int check_ws(void* workspace, size_t workspace_bytes, int64_t B, int64_t H, int64_t T) {
+    if (!workspace) return fail(-1, "null workspace");
+    if (((uintptr_t)workspace & 255u) != 0) return fail(-1, "workspace must be 256-byte aligned");
+    const size_t need = carve(nullptr, B, H, T).bytes;
+    if (workspace_bytes < need) return fail(-1, "workspace too small: %zu bytes given, %zu needed", workspace_bytes, need);
+    return 0;
 }
 
 }  // namespace
 
-// Dispatch on (head_dim, dtype) for the four templated stages.
+// Dispatch on (head_dim, dtype) for the templated stages.
 #define NNFA_DISPATCH(FN, D, DT, ...)                                 \
     ((D) == 64 ? ((DT) == kBF16 ? FN<64, kBF16>(__VA_ARGS__)          \
                                 : FN<64, kF16>(__VA_ARGS__))          \
@@ -704,11 +807,13 @@ int post_impl(const Workspace& w, void* dq, void* dk, void* dv, int64_t B, int64
 
 NNFA_API const char* nn_fa_last_error(void) { return g_last_error.c_str(); }
 
-NNFA_API int nn_fa_abi_version(void) { return 2; }
+NNFA_API int nn_fa_abi_version(void) { return 3; }
 
 NNFA_API size_t nn_fa_bwd_workspace_size(int64_t B, int64_t H, int64_t KVH, int64_t T, int64_t D) {
-    if (B < 0 || H < 0 || KVH < 0 || T < 0 || D < 0) return 0;
-    return carve(nullptr, B, H, KVH, T, D).bytes;
+    (void)KVH;
+    (void)D;
+    if (B < 0 || H < 0 || T < 0) return 0;
+    return carve(nullptr, B, H, T).bytes;
 }
 
 NNFA_API int nn_fa_fwd(const void* q, const void* k, const void* v, void* o, float* lse, int64_t B, int64_t H,
@@ -721,60 +826,51 @@ NNFA_API int nn_fa_fwd(const void* q, const void* k, const void* v, void* o, flo
     return NNFA_DISPATCH(fwd_impl, D, dtype, q, k, v, o, lse, B, H, KVH, T, scale, (hipStream_t)stream);
 }
 
-static int check_ws(void* workspace, size_t workspace_bytes, int64_t B, int64_t H, int64_t KVH, int64_t T, int64_t D) {
-    if (!workspace) return fail(-1, "null workspace");
-    if (((uintptr_t)workspace & 255u) != 0) return fail(-1, "workspace must be 256-byte aligned");
-    const size_t need = nn_fa_bwd_workspace_size(B, H, KVH, T, D);
-    if (workspace_bytes < need)
-        return fail(-1, "workspace too small: %zu bytes given, %zu needed", workspace_bytes, need);
-    return 0;
-}
-
 NNFA_API int nn_fa_bwd_pre(const void* o, const void* dO, const float* lse, void* workspace, size_t workspace_bytes,
                            int64_t B, int64_t H, int64_t KVH, int64_t T, int64_t D, int dtype, void* stream) {
     g_last_error.clear();
     if (int e = check_dims(B, H, KVH, T, D, dtype)) return e;
     if (B == 0 || T == 0) return 0;
-    if (int e = check_ws(workspace, workspace_bytes, B, H, KVH, T, D)) return e;
+    if (int e = check_ws(workspace, workspace_bytes, B, H, T)) return e;
     if (!o || !dO || !lse) return fail(-1, "null pointer argument");
     if (!aligned16(o) || !aligned16(dO)) return fail(-1, "inputs must be 16-byte aligned");
-    const Workspace w = carve(workspace, B, H, KVH, T, D);
+    const Workspace w = carve(workspace, B, H, T);
     return NNFA_DISPATCH(pre_impl, D, dtype, o, dO, lse, w, B, H, KVH, T, (hipStream_t)stream);
 }
 
-NNFA_API int nn_fa_bwd_main(const void* q, const void* k, const void* v, const void* dO, void* workspace,
-                            size_t workspace_bytes, int64_t B, int64_t H, int64_t KVH, int64_t T, int64_t D, int dtype,
-                            float scale, void* stream) {
+NNFA_API int nn_fa_bwd_dkdv(const void* q, const void* k, const void* v, const void* dO, const void* workspace,
+                            size_t workspace_bytes, void* dk, void* dv, int64_t B, int64_t H, int64_t KVH, int64_t T,
+                            int64_t D, int dtype, float scale, void* stream) {
     g_last_error.clear();
     if (int e = check_dims(B, H, KVH, T, D, dtype)) return e;
     if (B == 0 || T == 0) return 0;
-    if (int e = check_ws(workspace, workspace_bytes, B, H, KVH, T, D)) return e;
-    if (!q || !k || !v || !dO) return fail(-1, "null pointer argument");
-    if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(dO))
+    if (int e = check_ws((void*)workspace, workspace_bytes, B, H, T)) return e;
+    if (!q || !k || !v || !dO || !dk || !dv) return fail(-1, "null pointer argument");
+    if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(dO) || !aligned16(dk) || !aligned16(dv))
         return fail(-1, "inputs must be 16-byte aligned");
-    const Workspace w = carve(workspace, B, H, KVH, T, D);
-    return NNFA_DISPATCH(main_impl, D, dtype, q, k, v, dO, w, B, H, KVH, T, scale, (hipStream_t)stream);
+    const Workspace w = carve((void*)workspace, B, H, T);
+    return NNFA_DISPATCH(dkdv_impl, D, dtype, q, k, v, dO, w, dk, dv, B, H, KVH, T, scale, (hipStream_t)stream);
 }
 
-NNFA_API int nn_fa_bwd_post(const void* workspace, size_t workspace_bytes, void* dq, void* dk, void* dv, int64_t B,
-                            int64_t H, int64_t KVH, int64_t T, int64_t D, int dtype, float scale, void* stream) {
+NNFA_API int nn_fa_bwd_dq(const void* q, const void* k, const void* v, const void* dO, const void* workspace,
+                          size_t workspace_bytes, void* dq, int64_t B, int64_t H, int64_t KVH, int64_t T, int64_t D,
+                          int dtype, float scale, void* stream) {
     g_last_error.clear();
     if (int e = check_dims(B, H, KVH, T, D, dtype)) return e;
     if (B == 0 || T == 0) return 0;
-    if (int e = check_ws((void*)workspace, workspace_bytes, B, H, KVH, T, D)) return e;
-    if (!dq || !dk || !dv) return fail(-1, "null pointer argument");
-    if (!aligned16(dq) || !aligned16(dk) || !aligned16(dv)) return fail(-1, "outputs must be 16-byte aligned");
-    const Workspace w = carve((void*)workspace, B, H, KVH, T, D);
-    hipStream_t st = (hipStream_t)stream;
-    return dtype == kBF16 ? post_impl<kBF16>(w, dq, dk, dv, B, H, KVH, T, D, scale, st)
-                          : post_impl<kF16>(w, dq, dk, dv, B, H, KVH, T, D, scale, st);
+    if (int e = check_ws((void*)workspace, workspace_bytes, B, H, T)) return e;
+    if (!q || !k || !v || !dO || !dq) return fail(-1, "null pointer argument");
+    if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(dO) || !aligned16(dq))
+        return fail(-1, "inputs must be 16-byte aligned");
+    const Workspace w = carve((void*)workspace, B, H, T);
+    return NNFA_DISPATCH(dq_impl, D, dtype, q, k, v, dO, w, dq, B, H, KVH, T, scale, (hipStream_t)stream);
 }
 
 NNFA_API int nn_fa_bwd(const void* dO, const void* q, const void* k, const void* v, const void* o, const float* lse,
                        void* dq, void* dk, void* dv, void* workspace, size_t workspace_bytes, int64_t B, int64_t H,
                        int64_t KVH, int64_t T, int64_t D, int dtype, float scale, void* stream) {
     if (int e = nn_fa_bwd_pre(o, dO, lse, workspace, workspace_bytes, B, H, KVH, T, D, dtype, stream)) return e;
-    if (int e = nn_fa_bwd_main(q, k, v, dO, workspace, workspace_bytes, B, H, KVH, T, D, dtype, scale, stream))
+    if (int e = nn_fa_bwd_dkdv(q, k, v, dO, workspace, workspace_bytes, dk, dv, B, H, KVH, T, D, dtype, scale, stream))
         return e;
-    return nn_fa_bwd_post(workspace, workspace_bytes, dq, dk, dv, B, H, KVH, T, D, dtype, scale, stream);
+    return nn_fa_bwd_dq(q, k, v, dO, workspace, workspace_bytes, dq, B, H, KVH, T, D, dtype, scale, stream);
 }
