@@ -42,6 +42,7 @@ sys.path.insert(0, str(ROOT))
 METRIC = "causal GQA attn fwd+bwd TFLOP/s at T=1024; % of BF16 MFMA peak"
 PEAK_TFLOPS = 2500.0  # MI355X dense BF16/FP16 MFMA, published
 PEAK_HBM_GBPS = 8000.0
+COPY_CALIB_BYTES = 256 << 20  # size of the calibration copy run by --profile-only
 
 
 def parse():
@@ -177,7 +178,13 @@ def main():
     ms = timed(step_abi, args.steps)
     op_ms = timed(step_op, args.steps)
     if args.profile_only:
-        print(json.dumps({"ms_per_step": ms, "op_ms_per_step": op_ms}), flush=True)
+        # A plain device copy of known size, for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE readings.
+        src = torch.empty(COPY_CALIB_BYTES // 2, dtype=torch.bfloat16, device=dev).fill_(1.0)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"ms_per_step": ms, "op_ms_per_step": op_ms, "copy_calib_bytes": COPY_CALIB_BYTES}), flush=True)
         return
 
     # ---- each kernel alone, HIP events on the launch stream ----
@@ -219,6 +226,15 @@ def main():
     dominant = max(("fwd", "bwd_dkdv", "bwd_dq"), key=lambda n: kern_us[n])
     kernel_names = {"fwd": "fa_fwd_kernel", "bwd_dkdv": "fa_bwd_dkdv_kernel", "bwd_dq": "fa_bwd_dq_kernel"}
 
+    # HBM bytes per launch of the dominant kernel, from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE
+    # summary of this workload (profiles/), when one exists for it.
+    traffic = None
+    tfile = ROOT / "profiles" / f"fa_causal_gqa_b{B}_t{T}_{args.dtype}.traffic.json"
+    if tfile.exists() and (H, KVH, D) == (12, 4, 64):
+        measured = json.loads(tfile.read_text())
+        key = f"{kernel_names[dominant]}<{D},{args.dtype}>"
+        traffic = round(measured[key]) if key in measured else None
+
     value = f_all / (ms * 1e-3) / 1e12
     props = torch.cuda.get_device_properties(dev)
     out = {
@@ -248,7 +264,7 @@ def main():
             "peak": PEAK_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(kern_tflops[dominant] / PEAK_TFLOPS, 4),
-            "traffic": None,
+            "traffic": traffic,
         },
         "kernels": {
             "fwd_us": round(kern_us["fwd"], 2),
