@@ -192,7 +192,7 @@ def main():
         "fwd": lambda: L.nn_fa_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(),
                                    B, H, KVH, T, D, dt_code, scale, sp),
         "bwd_pre": lambda: L.nn_fa_bwd_pre(o.data_ptr(), do.data_ptr(), lse.data_ptr(), ws.data_ptr(), ws_bytes,
-                                           B, H, KVH, T, D, dt_code, sp),
+                                           B, H, KVH, T, D, dt_code, scale, sp),
         "bwd_dkdv": lambda: L.nn_fa_bwd_dkdv(q.data_ptr(), k.data_ptr(), v.data_ptr(), do.data_ptr(), ws.data_ptr(),
                                              ws_bytes, dk.data_ptr(), dv.data_ptr(), B, H, KVH, T, D, dt_code, scale, sp),
         "bwd_dq": lambda: L.nn_fa_bwd_dq(q.data_ptr(), k.data_ptr(), v.data_ptr(), do.data_ptr(), ws.data_ptr(),
@@ -213,7 +213,7 @@ def main():
 
     e = 2  # bytes per 16-bit element
     pre_alg_bytes = 2 * B * H * T * D * e + 4 * B * H * T
-    pre_all_bytes = pre_alg_bytes + 8 * B * H * T  # also reads lse and writes its base-2 copy
+    pre_all_bytes = pre_alg_bytes + 8 * B * H * T  # also reads lse and writes -lse/scale
     # Algorithmic FLOPs (8*D per causal pair for the backward) split by the products each kernel owns:
     # dV, dP, dK -> dk/dv kernel (6*D), dQ -> dq kernel (2*D); the dP and S recomputed by each are not counted.
     f_dkdv = 3.0 * B * H * D * T * (T + 1)

@@ -36,8 +36,8 @@ int nn_fa_fwd(const void* q, const void* k, const void* v, void* o, float* lse,
               int64_t B, int64_t H, int64_t KVH, int64_t T, int64_t D,
               int dtype, float scale, void* stream);
 
-/* Bytes of device workspace the backward needs: D = rowsum(dO * o) and a base-2 copy of lse,
- * one fp32 each per query row. The caller allocates it, 256-byte aligned; its contents on entry
+/* Bytes of device workspace the backward needs: -rowsum(dO * o) and -lse / scale, one fp32 each
+ * per query row. The caller allocates it, 256-byte aligned; its contents on entry
  * do not matter. */
 size_t nn_fa_bwd_workspace_size(int64_t B, int64_t H, int64_t KVH, int64_t T, int64_t D);
 
@@ -53,10 +53,11 @@ int nn_fa_bwd(const void* dO, const void* q, const void* k, const void* v, const
               int64_t B, int64_t H, int64_t KVH, int64_t T, int64_t D,
               int dtype, float scale, void* stream);
 
-/* Backward, stage 1: D = rowsum(dO * o) and lse * log2(e), fp32, into the workspace.
+/* Backward, stage 1: -D = -rowsum(dO * o) and -lse / scale, fp32, into the workspace.
  * Replaces the ATen preprocessing inside flash_bwd, flash_attn.cu:387-391. */
 int nn_fa_bwd_pre(const void* o, const void* dO, const float* lse, void* workspace, size_t workspace_bytes,
-                  int64_t B, int64_t H, int64_t KVH, int64_t T, int64_t D, int dtype, void* stream);
+                  int64_t B, int64_t H, int64_t KVH, int64_t T, int64_t D, int dtype, float scale,
+                  void* stream);
 
 /* Backward, stage 2: dk and dv (keys outer; recomputes P from the workspace's lse and uses its D).
  * Needs the workspace prepared by nn_fa_bwd_pre. Together with stage 3 it replaces

@@ -41,6 +41,7 @@
 #include <string.h>
 
 #include <string>
+#include <type_traits>
 
 #include "nanonemo_fa.h"
 
@@ -119,6 +120,12 @@ __device__ inline u16x8 pack8(const f32x16& a, int base) {
 }
 
 __device__ inline u16x8 cat4(u16x4 a, u16x4 b) { return __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7); }
+typedef float f32x8 __attribute__((ext_vector_type(8)));
+__device__ inline f32x16 cat16(f32x4 a, f32x4 b, f32x4 c, f32x4 d) {
+    const f32x8 ab = __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7);
+    const f32x8 cd = __builtin_shufflevector(c, d, 0, 1, 2, 3, 4, 5, 6, 7);
+    return __builtin_shufflevector(ab, cd, 0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15);
+}
 __device__ inline u16x8 ld8(const u16* p) { return *reinterpret_cast<const u16x8*>(p); }
 
 // Row-major LDS tiles of W 16-bit columns store 16-byte chunk c of row r at chunk position
@@ -253,61 +260,94 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_kernel(const u16* __restrict__ 
         dma_rows<HD, BN, NW>(Kp, it * BN, T, kb, wave, lane);
         dma_rows<HD, BN, NW>(Vp, it * BN, T, vb, wave, lane);
     };
+    // One 128-key tile as four 32-key sub-tiles, software-pipelined so that the matrix unit and the
+    // VALU have independent work in the same stretch of straight-line code:
+    //   * K operands of sub-tile t+2 are read from LDS while sub-tile t is processed, so the S^T
+    //     MFMAs of sub-tile t+1, issued at the top of step t, never wait on LDS;
+    //   * the V^T operands of step t are read before its exponentials;
+    //   * the running max is updated without branching (a stale max is kept unless a row grows by
+    //     more than 2^8); only the rare rescale of O is a branch, placed just before the P V MFMAs.
+    // MASK: the tile crosses the diagonal or T.
+    auto tile = [&](auto mask_tag, int k0, const u16* kb, const u16* vb) {
+        constexpr bool MASK = decltype(mask_tag)::value;
+        const int lim = min(qrow, T - 1) - k0 - 4 * hh;  // key offsets beyond this are masked
+        const int nt = MASK ? min(NT, (qw + 31 - k0) / 32 + 1) : NT;  // sub-tiles with a visible key
+        auto kops = [&](int t, u16x8* kq) {
+#pragma unroll
+            for (int ks = 0; ks < NS; ++ks) kq[ks] = ld8(kb + 32 * t * HD + koff[ks]);
+        };
+        auto scores = [&](const u16x8* kq) {
+            f32x16 a = f32x16{};
+#pragma unroll
+            for (int ks = 0; ks < NS; ++ks) a = E::mfma(kq[ks], qf[ks], a);
+            return a;
+        };
+        u16x8 kq0[NS], kq1[NS];
+        kops(0, kq0);
+        f32x16 cur = scores(kq0);
+        if (!MASK || nt > 1) kops(1, kq1);
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            if (MASK && t >= nt) break;
+            u16x8* kn = (t & 1) ? kq0 : kq1;  // operands of sub-tile t+1, read one step ago
+            f32x16 nxt = f32x16{};
+            if (t + 1 < NT && (!MASK || t + 1 < nt)) nxt = scores(kn);
+            if (t + 2 < NT && (!MASK || t + 2 < nt)) kops(t + 2, (t & 1) ? kq1 : kq0);
+            u16x8 va[2][ND];
+#pragma unroll
+            for (int half = 0; half < 2; ++half)
+#pragma unroll
+                for (int dt = 0; dt < ND; ++dt) {
+                    const u16* vc = vb + 16 * (2 * t + half) * HD;
+                    va[half][dt] = cat4(ld_tr(vc + voff[dt][0]), ld_tr(vc + voff[dt][1]));
+                }
+            // cur[i] = score of query qrow against key k0 + 32t + (i/4)*8 + 4hh + i%4.
+            if (MASK) {
+#pragma unroll
+                for (int i = 0; i < 16; ++i) cur[i] = (32 * t + (i >> 2) * 8 + (i & 3) > lim) ? -INFINITY : cur[i];
+            }
+            float mx = cur[0];
+#pragma unroll
+            for (int i = 1; i < 16; ++i) mx = fmaxf(mx, cur[i]);
+            mx = pair_max(mx);
+            const bool grow = (mx - m) * sl2 > kRescaleLog2;  // always true while m = -inf
+            const float mnew = grow ? mx : m;
+            const float corr = fast_exp2((m - mnew) * sl2);  // 0 on the first tile, 1 where m is kept
+            m = mnew;
+            lsum *= corr;
+            const float mb = m * sl2;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) cur[i] = fast_exp2(fmaf(cur[i], sl2, -mb));
+            u16x8 pf[2];
+#pragma unroll
+            for (int half = 0; half < 2; ++half) {
+                pf[half] = pack8<DT>(cur, 8 * half);  // P^T chunk 2t+half: keys 16(2t+half) + (j/4)*8 + 4hh + j%4
+                const u32x4 pw = __builtin_bit_cast(u32x4, pf[half]);
+                lsum = E::add_pair(pw[0], lsum);
+                lsum = E::add_pair(pw[1], lsum);
+                lsum = E::add_pair(pw[2], lsum);
+                lsum = E::add_pair(pw[3], lsum);
+            }
+            // lsum >= 0 always holds; testing it keeps this branch after the exponentials, so they
+            // share a scheduling region with the S^T MFMAs of sub-tile t+1.
+            if (__builtin_amdgcn_ballot_w64(grow && lsum >= 0.f)) {
+#pragma unroll
+                for (int dt = 0; dt < ND; ++dt) oacc[dt] *= corr;
+            }
+#pragma unroll
+            for (int half = 0; half < 2; ++half)
+#pragma unroll
+                for (int dt = 0; dt < ND; ++dt) oacc[dt] = E::mfma(va[half][dt], pf[half], oacc[dt]);
+            cur = nxt;
+        }
+    };
     auto step = [&](int it, const u16* kb, const u16* vb) {
         const int k0 = it * BN;
         if (qw >= T || k0 > qw + 31) return;  // no visible key in this tile for this wave
-        f32x16 s[NT];
-#pragma unroll
-        for (int t = 0; t < NT; ++t) {
-            s[t] = f32x16{};
-#pragma unroll
-            for (int ks = 0; ks < NS; ++ks)
-                s[t] = E::mfma(ld8(kb + 32 * t * HD + koff[ks]), qf[ks], s[t]);
-        }
-        // s[t][i] = score of query qrow against key k0 + 32t + (i/4)*8 + 4hh + i%4.
-        if (k0 + BN - 1 > qw || k0 + BN > T) {
-            const int lim = min(qrow, T - 1) - k0 - 4 * hh;
-#pragma unroll
-            for (int t = 0; t < NT; ++t)
-#pragma unroll
-                for (int i = 0; i < 16; ++i)
-                    s[t][i] = (32 * t + (i >> 2) * 8 + (i & 3) > lim) ? -INFINITY : s[t][i];
-        }
-        float mx = -INFINITY;
-#pragma unroll
-        for (int t = 0; t < NT; ++t)
-#pragma unroll
-            for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[t][i]);
-        mx = pair_max(mx);
-        const bool grow = (mx - m) * sl2 > kRescaleLog2;  // always true while m = -inf
-        if (__builtin_amdgcn_ballot_w64(grow)) {
-            const float mnew = grow ? mx : m;
-            const float corr = fast_exp2((m - mnew) * sl2);  // 0 on the first tile, 1 where m is kept
-            lsum *= corr;
-#pragma unroll
-            for (int dt = 0; dt < ND; ++dt) oacc[dt] *= corr;
-            m = mnew;
-        }
-        const float mb = m * sl2;
-#pragma unroll
-        for (int c = 0; c < BN / 16; ++c) {
-            f32x16& st = s[c >> 1];
-            const int base = 8 * (c & 1);
-#pragma unroll
-            for (int j = 0; j < 8; ++j) st[base + j] = fast_exp2(fmaf(st[base + j], sl2, -mb));
-            const u16x8 pf = pack8<DT>(st, base);
-            const u32x4 pw = __builtin_bit_cast(u32x4, pf);
-            lsum = E::add_pair(pw[0], lsum);
-            lsum = E::add_pair(pw[1], lsum);
-            lsum = E::add_pair(pw[2], lsum);
-            lsum = E::add_pair(pw[3], lsum);
-            // P^T chunk c holds keys 16c + (j/4)*8 + 4hh + j%4; V^T must use the same order.
-#pragma unroll
-            for (int dt = 0; dt < ND; ++dt) {
-                const u16x8 va = cat4(ld_tr(vb + 16 * c * HD + voff[dt][0]), ld_tr(vb + 16 * c * HD + voff[dt][1]));
-                oacc[dt] = E::mfma(va, pf, oacc[dt]);
-            }
-        }
+        if (k0 + BN - 1 > qw || k0 + BN > T)
+            tile(std::true_type{}, k0, kb, vb);
+        else
+            tile(std::false_type{}, k0, kb, vb);
     };
 
     issue(0, kA, vA);
@@ -340,12 +380,14 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_kernel(const u16* __restrict__ 
 }
 
 // ------------------------------------------------------------------------------------------
-// Backward, preprocessing: D = rowsum(dO * O) and lse2 = lse * log2(e), fp32, in one pass.
+// Backward, preprocessing, one pass over dO and O: nD = -rowsum(dO * O) and nL = -lse / scale, fp32.
+// Both enter the backward products as accumulator initial values: S - lse/scale and dP - D come
+// straight out of the MFMAs, so P = exp2((S - lse/scale) * scale * log2(e)) and dS = P (dP - D).
 // ------------------------------------------------------------------------------------------
 template <int HD, int DT>
 __global__ __launch_bounds__(256) void fa_bwd_pre_kernel(const u16* __restrict__ O, const u16* __restrict__ dO,
-                                                         const float* __restrict__ LSE, float* __restrict__ Dvec,
-                                                         float* __restrict__ Lse2, int64_t rows) {
+                                                         const float* __restrict__ LSE, float* __restrict__ nDvec,
+                                                         float* __restrict__ nLvec, int64_t rows, float inv_scale) {
     using E = Elem<DT>;
     constexpr int TPR = HD / 8;  // threads per row
     const int64_t gtid = (int64_t)blockIdx.x * 256 + threadIdx.x;
@@ -360,8 +402,8 @@ __global__ __launch_bounds__(256) void fa_bwd_pre_kernel(const u16* __restrict__
 #pragma unroll
     for (int off = TPR / 2; off > 0; off >>= 1) acc += __shfl_xor(acc, off);
     if (row < rows && c == 0) {
-        Dvec[row] = acc;
-        Lse2[row] = LSE[row] * kLog2e;
+        nDvec[row] = -acc;
+        nLvec[row] = -LSE[row] * inv_scale;
     }
 }
 
@@ -374,14 +416,17 @@ __global__ __launch_bounds__(256) void fa_bwd_pre_kernel(const u16* __restrict__
 // the 4 partial dK / dV are summed through LDS and stored once in the output dtype (no atomics,
 // no fp32 round trip through HBM). A block takes unit j and unit nkb-1-j, so every block
 // carries the same causal work. Per tile:
-//   S = Q K^T, dP = dO V^T             (A = Q / dO rows from LDS, B = K / V registers)
-//   P = exp2(S*sl2 - lse2), dS = P (dP - D)
-//   dV^T += dO^T P, dK^T += Q^T dS     (A = columns of the Q / dO tiles, B = P / dS registers)
+//   S' = Q K^T - lse/scale, dP' = dO V^T - D   (A = Q / dO rows from LDS, B = K / V registers;
+//                                              the accumulators start from -lse/scale and -D)
+//   P = exp2(S' * sl2), dS = P dP'
+//   dV^T += dO^T P, dK^T += Q^T dS             (A = columns of the Q / dO tiles, B = P / dS registers)
+// Every LDS read of a 32-query step is issued before its products, so the MFMAs do not wait on
+// LDS one by one.
 // ------------------------------------------------------------------------------------------
 template <int HD, int DT>
 __global__ __launch_bounds__(512, 1) void fa_bwd_dkdv_kernel(
     const u16* __restrict__ Q, const u16* __restrict__ K, const u16* __restrict__ V, const u16* __restrict__ dO,
-    const float* __restrict__ Lse2, const float* __restrict__ Dvec, u16* __restrict__ dK, u16* __restrict__ dV,
+    const float* __restrict__ nLvec, const float* __restrict__ nDvec, u16* __restrict__ dK, u16* __restrict__ dV,
     int BKV, int H, int KVH, int T, int nkb, int nqt, float sl2, float scale) {
     using E = Elem<DT>;
     constexpr int BNK = 64, BM = 64, NG = 4, GW = 2;
@@ -394,7 +439,7 @@ __global__ __launch_bounds__(512, 1) void fa_bwd_dkdv_kernel(
     __shared__ __attribute__((aligned(16))) u16 oA[NG * QT];
     __shared__ __attribute__((aligned(16))) u16 qB[NG * QT];
     __shared__ __attribute__((aligned(16))) u16 oB[NG * QT];
-    __shared__ __attribute__((aligned(16))) float lA[NG * 2 * BM];  // per group: lse2 | D
+    __shared__ __attribute__((aligned(16))) float lA[NG * 2 * BM];  // per group: -lse/scale | -D
     __shared__ __attribute__((aligned(16))) float lB[NG * 2 * BM];
 
     const int bid = blockIdx.x;
@@ -441,8 +486,8 @@ __global__ __launch_bounds__(512, 1) void fa_bwd_dkdv_kernel(
             dma_rows<HD, BM, GW>(dO + qoff, qt * BM, T, os + gi * QT, wk, lane);
             const int q = min(qt * BM + (gtid & (BM - 1)), T - 1);
             const size_t ro = ((size_t)b * H + hq) * T + q;
-            if (gtid < BM) lse_r = Lse2[ro];
-            else d_r = Dvec[ro];
+            if (gtid < BM) lse_r = nLvec[ro];
+            else d_r = nDvec[ro];
         };
         auto compute = [&](int itn, const u16* qs, const u16* os, const float* ls) {
             const int g = itn / nq, qt = qt_first + itn - g * nq;
@@ -455,27 +500,44 @@ __global__ __launch_bounds__(512, 1) void fa_bwd_dkdv_kernel(
             const int qlim = key - qbase - 4 * hh;  // query offsets below this are in the future of the key
 #pragma unroll 1
             for (int qh = 0; qh < 2; ++qh) {
-                f32x16 s = f32x16{}, dp = f32x16{};
                 const u16* qrow = qb_ + 32 * qh * HD;
                 const u16* orow = ob_ + 32 * qh * HD;
+                const float* lq = lb_ + 32 * qh + 4 * hh;
+                // All LDS reads of this 32-query step first: Q / dO rows, -lse/scale and -D as the
+                // accumulators' initial values (element i: query 32qh + (i/4)*8 + 4hh + i%4), and
+                // the Q^T / dO^T columns of both 16-query chunks.
+                u16x8 qa[NS], oa[NS];
 #pragma unroll
                 for (int ks = 0; ks < NS; ++ks) {
-                    s = E::mfma(ld8(qrow + qroff[ks]), kf[ks], s);
-                    dp = E::mfma(ld8(orow + qroff[ks]), vf[ks], dp);
+                    qa[ks] = ld8(qrow + qroff[ks]);
+                    oa[ks] = ld8(orow + qroff[ks]);
                 }
-                // s[i]: query qbase + 32qh + (i/4)*8 + 4hh + i%4 against this lane's key.
-                const float* lq = lb_ + 32 * qh + 4 * hh;
+                const f32x4* lv = reinterpret_cast<const f32x4*>(lq);
+                const f32x4* dv4 = reinterpret_cast<const f32x4*>(lq + BM);
+                f32x16 s = cat16(lv[0], lv[2], lv[4], lv[6]);    // +8 floats per group of 4 rows
+                f32x16 dp = cat16(dv4[0], dv4[2], dv4[4], dv4[6]);
+                u16x8 gcol[2][ND], qcol[2][ND];
+                auto load_cols = [&](int half) {
+                    const u16* oc = ob_ + 16 * (2 * qh + half) * HD;
+                    const u16* qc = qb_ + 16 * (2 * qh + half) * HD;
 #pragma unroll
-                for (int g4 = 0; g4 < 4; ++g4) {
-                    const f32x4 L = *reinterpret_cast<const f32x4*>(lq + 8 * g4);
-                    const f32x4 Dd = *reinterpret_cast<const f32x4*>(lq + BM + 8 * g4);
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        const int i = 4 * g4 + r;
-                        const float p = fast_exp2(fmaf(s[i], sl2, -L[r]));
-                        dp[i] = p * (dp[i] - Dd[r]);
-                        s[i] = p;
+                    for (int dt = 0; dt < ND; ++dt) {
+                        gcol[half][dt] = cat4(ld_tr(oc + qcoff[dt][0]), ld_tr(oc + qcoff[dt][1]));
+                        qcol[half][dt] = cat4(ld_tr(qc + qcoff[dt][0]), ld_tr(qc + qcoff[dt][1]));
                     }
+                };
+                load_cols(0);
+#pragma unroll
+                for (int ks = 0; ks < NS; ++ks) {
+                    s = E::mfma(qa[ks], kf[ks], s);
+                    dp = E::mfma(oa[ks], vf[ks], dp);
+                }
+                load_cols(1);  // in flight while the softmax runs
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    const float p = fast_exp2(s[i] * sl2);
+                    dp[i] *= p;
+                    s[i] = p;
                 }
                 if (need_mask) {  // visible iff key <= q, q < T and key < T
                     const int qrem = T - qbase - 32 * qh - 4 * hh;  // query offsets >= this are past T
@@ -490,15 +552,13 @@ __global__ __launch_bounds__(512, 1) void fa_bwd_dkdv_kernel(
                 }
 #pragma unroll
                 for (int half = 0; half < 2; ++half) {
-                    const int qc = 2 * qh + half;  // 16-query chunk: queries 16qc + (j/4)*8 + 4hh + j%4
+                    // 16-query chunk 2qh + half: queries 16(2qh+half) + (j/4)*8 + 4hh + j%4
                     const u16x8 pf = pack8<DT>(s, 8 * half);
                     const u16x8 sf = pack8<DT>(dp, 8 * half);
-                    const u16* ocol = ob_ + 16 * qc * HD;
-                    const u16* qcol = qb_ + 16 * qc * HD;
 #pragma unroll
                     for (int dt = 0; dt < ND; ++dt) {
-                        dv[dt] = E::mfma(cat4(ld_tr(ocol + qcoff[dt][0]), ld_tr(ocol + qcoff[dt][1])), pf, dv[dt]);
-                        dk[dt] = E::mfma(cat4(ld_tr(qcol + qcoff[dt][0]), ld_tr(qcol + qcoff[dt][1])), sf, dk[dt]);
+                        dv[dt] = E::mfma(gcol[half][dt], pf, dv[dt]);
+                        dk[dt] = E::mfma(qcol[half][dt], sf, dk[dt]);
                     }
                 }
             }
@@ -562,18 +622,18 @@ __global__ __launch_bounds__(512, 1) void fa_bwd_dkdv_kernel(
 
 // ------------------------------------------------------------------------------------------
 // Backward, dQ. Shaped like the forward: block = 4 waves = 128 query rows of one (batch, head),
-// 64-key tiles of K and V double-buffered in LDS by DMA, Q and dO rows in registers, lse2 and D
+// 64-key tiles of K and V double-buffered in LDS by DMA, Q and dO rows in registers, lse and D
 // per lane. Per tile:
 //   S^T = K Q^T, dP^T = V dO^T          (A = K / V rows from LDS, B = Q / dO registers)
-//   dS^T = exp2(S^T*sl2 - lse2) (dP^T - D)
+//   dS^T = exp2((S^T - lse/scale) * sl2) (dP^T - D)
 //   dQ^T += K^T dS^T                    (A = columns of the K tile, B = dS^T registers)
 // dQ stays in registers for the whole key loop and is stored once, scaled, in the output dtype.
 // ------------------------------------------------------------------------------------------
 template <int HD, int DT>
 __global__ __launch_bounds__(256, 2) void fa_bwd_dq_kernel(const u16* __restrict__ Q, const u16* __restrict__ K,
                                                            const u16* __restrict__ V, const u16* __restrict__ dO,
-                                                           const float* __restrict__ Lse2,
-                                                           const float* __restrict__ Dvec, u16* __restrict__ dQ, int BH,
+                                                           const float* __restrict__ nLvec,
+                                                           const float* __restrict__ nDvec, u16* __restrict__ dQ, int BH,
                                                            int H, int KVH, int T, int nqb, float sl2, float scale) {
     using E = Elem<DT>;
     constexpr int BM = 128, BN = 64, NW = 4;
@@ -607,8 +667,8 @@ __global__ __launch_bounds__(256, 2) void fa_bwd_dq_kernel(const u16* __restrict
         qf[s] = ld8(Q + qoff + (size_t)qc_ * HD + 16 * s + 8 * hh);
         gf[s] = ld8(dO + qoff + (size_t)qc_ * HD + 16 * s + 8 * hh);
     }
-    const float lse2 = Lse2[(size_t)bh * T + qc_];
-    const float dd = Dvec[(size_t)bh * T + qc_];
+    const float nl2 = nLvec[(size_t)bh * T + qc_] * sl2;  // -lse * log2(e)
+    const float nd = nDvec[(size_t)bh * T + qc_];
 
     int koff[NS], kcol[ND][2];
 #pragma unroll
@@ -645,7 +705,7 @@ __global__ __launch_bounds__(256, 2) void fa_bwd_dq_kernel(const u16* __restrict
 #pragma unroll
         for (int t = 0; t < NT; ++t)
 #pragma unroll
-            for (int i = 0; i < 16; ++i) dp[t][i] = fast_exp2(fmaf(s[t][i], sl2, -lse2)) * (dp[t][i] - dd);
+            for (int i = 0; i < 16; ++i) dp[t][i] = fast_exp2(fmaf(s[t][i], sl2, nl2)) * (dp[t][i] + nd);
         if (k0 + BN - 1 > qw || k0 + BN > T) {
             const int lim = min(qrow, T - 1) - k0 - 4 * hh;
 #pragma unroll
@@ -725,10 +785,10 @@ int check_dims(int64_t B, int64_t H, int64_t KVH, int64_t T, int64_t D, int dtyp
     return 0;
 }
 
-// Backward workspace: D = rowsum(dO * o) and lse * log2(e), one fp32 per query row each.
+// Backward workspace: nD = -rowsum(dO * o) and nL = -lse / scale, one fp32 per query row each.
 struct Workspace {
-    float* D;
-    float* lse2;
+    float* nD;
+    float* nL;
     size_t bytes;
 };
 
@@ -737,8 +797,8 @@ size_t round256(size_t n) { return (n + 255) & ~(size_t)255; }
 Workspace carve(void* base, int64_t B, int64_t H, int64_t T) {
     const size_t vec = round256(4 * (size_t)B * H * T);
     Workspace w;
-    w.D = (float*)base;
-    w.lse2 = (float*)((char*)base + vec);
+    w.nD = (float*)base;
+    w.nL = (float*)((char*)base + vec);
     w.bytes = 2 * vec;
     return w;
 }
@@ -755,12 +815,12 @@ int fwd_impl(const void* q, const void* k, const void* v, void* o, float* lse, i
 
 template <int HD, int DT>
 int pre_impl(const void* o, const void* dO, const float* lse, const Workspace& w, int64_t B, int64_t H, int64_t KVH,
-             int64_t T, hipStream_t st) {
+             int64_t T, float scale, hipStream_t st) {
     (void)KVH;
     const int64_t rows = B * H * T;
     const int64_t blocks = (rows * (HD / 8) + 255) / 256;
-    fa_bwd_pre_kernel<HD, DT><<<dim3((unsigned)blocks), dim3(256), 0, st>>>((const u16*)o, (const u16*)dO, lse, w.D,
-                                                                           w.lse2, rows);
+    fa_bwd_pre_kernel<HD, DT><<<dim3((unsigned)blocks), dim3(256), 0, st>>>((const u16*)o, (const u16*)dO, lse, w.nD,
+                                                                           w.nL, rows, 1.0f / scale);
     return launch_status("fa_bwd_pre_kernel");
 }
 
@@ -772,7 +832,7 @@ int dkdv_impl(const void* q, const void* k, const void* v, const void* dO, const
     const int npairs = (nkb + 1) / 2;
     const int BKV = (int)(B * KVH);
     fa_bwd_dkdv_kernel<HD, DT><<<dim3(npairs * BKV), dim3(512), 0, st>>>(
-        (const u16*)q, (const u16*)k, (const u16*)v, (const u16*)dO, w.lse2, w.D, (u16*)dk, (u16*)dv, BKV, (int)H,
+        (const u16*)q, (const u16*)k, (const u16*)v, (const u16*)dO, w.nL, w.nD, (u16*)dk, (u16*)dv, BKV, (int)H,
         (int)KVH, (int)T, nkb, nqt, scale * kLog2e, scale);
     return launch_status("fa_bwd_dkdv_kernel");
 }
@@ -783,7 +843,7 @@ int dq_impl(const void* q, const void* k, const void* v, const void* dO, const W
     const int nqb = (int)((T + 127) / 128);
     const int BH = (int)(B * H);
     fa_bwd_dq_kernel<HD, DT><<<dim3(nqb * BH), dim3(256), 0, st>>>(
-        (const u16*)q, (const u16*)k, (const u16*)v, (const u16*)dO, w.lse2, w.D, (u16*)dq, BH, (int)H, (int)KVH,
+        (const u16*)q, (const u16*)k, (const u16*)v, (const u16*)dO, w.nL, w.nD, (u16*)dq, BH, (int)H, (int)KVH,
         (int)T, nqb, scale * kLog2e, scale);
     return launch_status("fa_bwd_dq_kernel");
 }
@@ -807,7 +867,7 @@ int check_ws(void* workspace, size_t workspace_bytes, int64_t B, int64_t H, int6
 
 NNFA_API const char* nn_fa_last_error(void) { return g_last_error.c_str(); }
 
-NNFA_API int nn_fa_abi_version(void) { return 3; }
+NNFA_API int nn_fa_abi_version(void) { return 4; }
 
 NNFA_API size_t nn_fa_bwd_workspace_size(int64_t B, int64_t H, int64_t KVH, int64_t T, int64_t D) {
     (void)KVH;
@@ -827,7 +887,8 @@ NNFA_API int nn_fa_fwd(const void* q, const void* k, const void* v, void* o, flo
 }
 
 NNFA_API int nn_fa_bwd_pre(const void* o, const void* dO, const float* lse, void* workspace, size_t workspace_bytes,
-                           int64_t B, int64_t H, int64_t KVH, int64_t T, int64_t D, int dtype, void* stream) {
+                           int64_t B, int64_t H, int64_t KVH, int64_t T, int64_t D, int dtype, float scale,
+                           void* stream) {
     g_last_error.clear();
     if (int e = check_dims(B, H, KVH, T, D, dtype)) return e;
     if (B == 0 || T == 0) return 0;
@@ -835,7 +896,8 @@ NNFA_API int nn_fa_bwd_pre(const void* o, const void* dO, const float* lse, void
     if (!o || !dO || !lse) return fail(-1, "null pointer argument");
     if (!aligned16(o) || !aligned16(dO)) return fail(-1, "inputs must be 16-byte aligned");
     const Workspace w = carve(workspace, B, H, T);
-    return NNFA_DISPATCH(pre_impl, D, dtype, o, dO, lse, w, B, H, KVH, T, (hipStream_t)stream);
+    if (!(scale > 0.f)) return fail(-1, "scale must be positive");
+    return NNFA_DISPATCH(pre_impl, D, dtype, o, dO, lse, w, B, H, KVH, T, scale, (hipStream_t)stream);
 }
 
 NNFA_API int nn_fa_bwd_dkdv(const void* q, const void* k, const void* v, const void* dO, const void* workspace,
@@ -869,7 +931,7 @@ NNFA_API int nn_fa_bwd_dq(const void* q, const void* k, const void* v, const voi
 NNFA_API int nn_fa_bwd(const void* dO, const void* q, const void* k, const void* v, const void* o, const float* lse,
                        void* dq, void* dk, void* dv, void* workspace, size_t workspace_bytes, int64_t B, int64_t H,
                        int64_t KVH, int64_t T, int64_t D, int dtype, float scale, void* stream) {
-    if (int e = nn_fa_bwd_pre(o, dO, lse, workspace, workspace_bytes, B, H, KVH, T, D, dtype, stream)) return e;
+    if (int e = nn_fa_bwd_pre(o, dO, lse, workspace, workspace_bytes, B, H, KVH, T, D, dtype, scale, stream)) return e;
     if (int e = nn_fa_bwd_dkdv(q, k, v, dO, workspace, workspace_bytes, dk, dv, B, H, KVH, T, D, dtype, scale, stream))
         return e;
     return nn_fa_bwd_dq(q, k, v, dO, workspace, workspace_bytes, dq, B, H, KVH, T, D, dtype, scale, stream);

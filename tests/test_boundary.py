@@ -42,7 +42,7 @@ def test_abi_version():
 def test_workspace_size():
     L = lib()
     B, H, KVH, T, D = 8, 12, 4, 1024, 64
-    vec = 4 * B * H * T  # D = rowsum(dO * o) and the base-2 lse, fp32 per query row
+    vec = 4 * B * H * T  # -rowsum(dO * o) and -lse/scale, fp32 per query row
     rnd = lambda n: (n + 255) // 256 * 256  # noqa: E731
     assert L.nn_fa_bwd_workspace_size(B, H, KVH, T, D) == 2 * rnd(vec)
     assert L.nn_fa_bwd_workspace_size(0, H, KVH, T, D) == 0
@@ -76,7 +76,7 @@ def test_c_abi_rejects_misaligned_and_small_workspace():
     assert rc != 0 and "workspace too small" in L.nn_fa_last_error().decode()
     rc = L.nn_fa_bwd_dq(16, 16, 16, 16, 256, 10, 16, 1, 4, 2, 16, 64, 1, 0.125, None)
     assert rc != 0 and "workspace too small" in L.nn_fa_last_error().decode()
-    rc = L.nn_fa_bwd_pre(16, 16, 16, 0, 1 << 20, 1, 4, 2, 16, 64, 1, None)
+    rc = L.nn_fa_bwd_pre(16, 16, 16, 0, 1 << 20, 1, 4, 2, 16, 64, 1, 0.125, None)
     assert rc != 0 and "null workspace" in L.nn_fa_last_error().decode()
 
 
