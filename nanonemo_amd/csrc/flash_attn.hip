@@ -243,7 +243,7 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_kernel(const u16* __restrict__ 
     f32x16 oacc[ND];
 #pragma unroll
     for (int dt = 0; dt < ND; ++dt) oacc[dt] = f32x16{};
-    float m = -INFINITY, lsum = 0.f;
+    float mb = -INFINITY, lsum = 0.f;
 
     // Per-lane LDS offsets: K row operand (key l32 + 32t, columns 16ks + 8hh; add 32t*HD) and
     // V^T column operand (keys 16c + 8x + 4hh.., column 32dt + l32; add 16c*HD).
@@ -266,7 +266,8 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_kernel(const u16* __restrict__ 
     //     MFMAs of sub-tile t+1, issued at the top of step t, never wait on LDS;
     //   * the V^T operands of step t are read before its exponentials;
     //   * the running max is updated without branching (a stale max is kept unless a row grows by
-    //     more than 2^8); only the rare rescale of O is a branch, placed just before the P V MFMAs.
+    //     more than 2^8); the rescale of the row sum and O, and its exponential, sit in a rare
+    //     branch placed just before the P V MFMAs.
     // MASK: the tile crosses the diagonal or T.
     auto tile = [&](auto mask_tag, int k0, const u16* kb, const u16* vb) {
         constexpr bool MASK = decltype(mask_tag)::value;
@@ -310,30 +311,35 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_kernel(const u16* __restrict__ 
 #pragma unroll
             for (int i = 1; i < 16; ++i) mx = fmaxf(mx, cur[i]);
             mx = pair_max(mx);
-            const bool grow = (mx - m) * sl2 > kRescaleLog2;  // always true while m = -inf
-            const float mnew = grow ? mx : m;
-            const float corr = fast_exp2((m - mnew) * sl2);  // 0 on the first tile, 1 where m is kept
-            m = mnew;
-            lsum *= corr;
-            const float mb = m * sl2;
+            // mb is the running max in base-2 units; it moves only when the row grows by more than
+            // 2^kRescaleLog2 (always on the first sub-tile, where mb = -inf).
+            const float mxb = mx * sl2;
+            const bool grow = mxb - mb > kRescaleLog2;
+            const float mold = mb;
+            mb = grow ? mxb : mb;
 #pragma unroll
             for (int i = 0; i < 16; ++i) cur[i] = fast_exp2(fmaf(cur[i], sl2, -mb));
             u16x8 pf[2];
+            float psum = 0.f;
 #pragma unroll
             for (int half = 0; half < 2; ++half) {
                 pf[half] = pack8<DT>(cur, 8 * half);  // P^T chunk 2t+half: keys 16(2t+half) + (j/4)*8 + 4hh + j%4
                 const u32x4 pw = __builtin_bit_cast(u32x4, pf[half]);
-                lsum = E::add_pair(pw[0], lsum);
-                lsum = E::add_pair(pw[1], lsum);
-                lsum = E::add_pair(pw[2], lsum);
-                lsum = E::add_pair(pw[3], lsum);
+                psum = E::add_pair(pw[0], psum);
+                psum = E::add_pair(pw[1], psum);
+                psum = E::add_pair(pw[2], psum);
+                psum = E::add_pair(pw[3], psum);
             }
-            // lsum >= 0 always holds; testing it keeps this branch after the exponentials, so they
-            // share a scheduling region with the S^T MFMAs of sub-tile t+1.
-            if (__builtin_amdgcn_ballot_w64(grow && lsum >= 0.f)) {
+            // Rare: some row's max moved, so its sum and O are rescaled by 2^(old - new) (0 on the
+            // first sub-tile, 1 for rows that kept theirs). psum >= 0 always holds; testing it keeps
+            // the branch after the exponentials, in one scheduling region with the next S^T MFMAs.
+            if (__builtin_amdgcn_ballot_w64(grow && psum >= 0.f)) {
+                const float corr = fast_exp2(mold - mb);
+                lsum *= corr;
 #pragma unroll
                 for (int dt = 0; dt < ND; ++dt) oacc[dt] *= corr;
             }
+            lsum += psum;
 #pragma unroll
             for (int half = 0; half < 2; ++half)
 #pragma unroll
@@ -375,7 +381,7 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_kernel(const u16* __restrict__ 
                 u32x2 w = {E::pack2(a[4 * g] * inv, a[4 * g + 1] * inv), E::pack2(a[4 * g + 2] * inv, a[4 * g + 3] * inv)};
                 *reinterpret_cast<u32x2*>(op + 32 * dt + 8 * g + 4 * hh) = w;
             }
-        if (hh == 0) LSE[(size_t)bh * T + qrow] = (m * sl2 + fast_log2(ltot)) * kLn2;
+        if (hh == 0) LSE[(size_t)bh * T + qrow] = (mb + fast_log2(ltot)) * kLn2;
     }
 }
 
