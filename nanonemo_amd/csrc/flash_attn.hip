@@ -495,14 +495,13 @@ __global__ __launch_bounds__(512, 1) void fa_bwd_dkdv_kernel(
             if (gtid < BM) lse_r = nLvec[ro];
             else d_r = nDvec[ro];
         };
-        auto compute = [&](int itn, const u16* qs, const u16* os, const float* ls) {
-            const int g = itn / nq, qt = qt_first + itn - g * nq;
-            const int qbase = qt * BM;
-            if (kw > qbase + BM - 1 || kw >= T) return;  // every key of this wave is in the future
+        // MASK: the iteration crosses the diagonal or T (a separate instantiation, so that unmasked
+        // iterations carry no per-element selects).
+        auto compute = [&](auto mask_tag, int qbase, const u16* qs, const u16* os, const float* ls) {
+            constexpr bool MASK = decltype(mask_tag)::value;
             const u16* qb_ = qs + gi * QT;
             const u16* ob_ = os + gi * QT;
             const float* lb_ = ls + gi * 2 * BM;
-            const bool need_mask = (kw + 31 > qbase) || (qbase + BM > T) || (kw + 32 > T);
             const int qlim = key - qbase - 4 * hh;  // query offsets below this are in the future of the key
 #pragma unroll 1
             for (int qh = 0; qh < 2; ++qh) {
@@ -545,7 +544,7 @@ __global__ __launch_bounds__(512, 1) void fa_bwd_dkdv_kernel(
                     dp[i] *= p;
                     s[i] = p;
                 }
-                if (need_mask) {  // visible iff key <= q, q < T and key < T
+                if (MASK) {  // visible iff key <= q, q < T and key < T
                     const int qrem = T - qbase - 32 * qh - 4 * hh;  // query offsets >= this are past T
                     const bool kin = key < T;
 #pragma unroll
@@ -574,7 +573,15 @@ __global__ __launch_bounds__(512, 1) void fa_bwd_dkdv_kernel(
             const int itn = NG * r + gi, nxt = itn + NG;
             __syncthreads();
             if (nxt < niter) issue(nxt, qn, on);
-            if (itn < niter) compute(itn, qs, os, ls);
+            if (itn < niter) {
+                const int g = itn / nq, qbase = (qt_first + itn - g * nq) * BM;
+                if (kw <= qbase + BM - 1 && kw < T) {  // else every key of this wave is in the future
+                    if ((kw + 31 > qbase) || (qbase + BM > T) || (kw + 32 > T))
+                        compute(std::true_type{}, qbase, qs, os, ls);
+                    else
+                        compute(std::false_type{}, qbase, qs, os, ls);
+                }
+            }
             wait_vmem();
             if (nxt < niter) ln[gi * 2 * BM + gtid] = gtid < BM ? lse_r : d_r;
         };
@@ -693,32 +700,42 @@ __global__ __launch_bounds__(256, 2) void fa_bwd_dq_kernel(const u16* __restrict
         dma_rows<HD, BN, NW>(Kp, it * BN, T, kb, wave, lane);
         dma_rows<HD, BN, NW>(Vp, it * BN, T, vb, wave, lane);
     };
-    auto step = [&](int it, const u16* kb, const u16* vb) {
-        const int k0 = it * BN;
-        if (qw >= T || k0 > qw + 31) return;  // no visible key in this tile for this wave
+    // -D enters as the initial value of every dP^T accumulator (the same for all of a lane's keys).
+    f32x16 ndv;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) ndv[i] = nd;
+    // MASK: the tile crosses the diagonal or T (a separate instantiation, so that unmasked tiles
+    // carry no per-element selects).
+    auto tile = [&](auto mask_tag, int k0, const u16* kb, const u16* vb) {
+        constexpr bool MASK = decltype(mask_tag)::value;
+        u16x8 ka[NT][NS], va[NT][NS];
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+#pragma unroll
+            for (int ks = 0; ks < NS; ++ks) {
+                ka[t][ks] = ld8(kb + 32 * t * HD + koff[ks]);
+                va[t][ks] = ld8(vb + 32 * t * HD + koff[ks]);
+            }
         f32x16 s[NT], dp[NT];
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
             s[t] = f32x16{};
-            dp[t] = f32x16{};
+            dp[t] = ndv;
 #pragma unroll
             for (int ks = 0; ks < NS; ++ks) {
-                s[t] = E::mfma(ld8(kb + 32 * t * HD + koff[ks]), qf[ks], s[t]);
-                dp[t] = E::mfma(ld8(vb + 32 * t * HD + koff[ks]), gf[ks], dp[t]);
+                s[t] = E::mfma(ka[t][ks], qf[ks], s[t]);
+                dp[t] = E::mfma(va[t][ks], gf[ks], dp[t]);
             }
         }
-        // s[t][i]: key k0 + 32t + (i/4)*8 + 4hh + i%4 against query qrow.
+        // s[t][i]: key k0 + 32t + (i/4)*8 + 4hh + i%4 against query qrow; dp[t][i] already holds dP - D.
+        const int lim = min(qrow, T - 1) - k0 - 4 * hh;
 #pragma unroll
         for (int t = 0; t < NT; ++t)
 #pragma unroll
-            for (int i = 0; i < 16; ++i) dp[t][i] = fast_exp2(fmaf(s[t][i], sl2, nl2)) * (dp[t][i] + nd);
-        if (k0 + BN - 1 > qw || k0 + BN > T) {
-            const int lim = min(qrow, T - 1) - k0 - 4 * hh;
-#pragma unroll
-            for (int t = 0; t < NT; ++t)
-#pragma unroll
-                for (int i = 0; i < 16; ++i) dp[t][i] = (32 * t + (i >> 2) * 8 + (i & 3) > lim) ? 0.f : dp[t][i];
-        }
+            for (int i = 0; i < 16; ++i) {
+                const float ds = fast_exp2(fmaf(s[t][i], sl2, nl2)) * dp[t][i];
+                dp[t][i] = (MASK && 32 * t + (i >> 2) * 8 + (i & 3) > lim) ? 0.f : ds;
+            }
 #pragma unroll
         for (int c = 0; c < BN / 16; ++c) {
             const u16x8 sf = pack8<DT>(dp[c >> 1], 8 * (c & 1));  // keys 16c + (j/4)*8 + 4hh + j%4
@@ -727,6 +744,14 @@ __global__ __launch_bounds__(256, 2) void fa_bwd_dq_kernel(const u16* __restrict
             for (int dt = 0; dt < ND; ++dt)
                 dq[dt] = E::mfma(cat4(ld_tr(kc + kcol[dt][0]), ld_tr(kc + kcol[dt][1])), sf, dq[dt]);
         }
+    };
+    auto step = [&](int it, const u16* kb, const u16* vb) {
+        const int k0 = it * BN;
+        if (qw >= T || k0 > qw + 31) return;  // no visible key in this tile for this wave
+        if (k0 + BN - 1 > qw || k0 + BN > T)
+            tile(std::true_type{}, k0, kb, vb);
+        else
+            tile(std::false_type{}, k0, kb, vb);
     };
 
     issue(0, kA, vA);
