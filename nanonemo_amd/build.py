@@ -38,10 +38,6 @@ HIPCC_FLAGS = [
     "-target-feature",
     "-Xclang",
     "-packed-fp32-ops",
-    # MFMA accumulators in ordinary VGPRs: without this the compiler parks them in AGPRs and
-    # copies every element through v_accvgpr_read/write around each softmax step.
-    "-mllvm",
-    "-amdgpu-mfma-vgpr-form=1",
     # Device code never relies on NaN semantics (masked scores are -inf, never NaN); without this
     # every fmaxf of an MFMA result is preceded by a canonicalising v_max_f32 x, x.
     "-Xarch_device",

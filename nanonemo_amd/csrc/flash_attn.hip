@@ -184,6 +184,14 @@ __device__ inline void dma_rows(const u16* __restrict__ g, int r0, int T, u16* l
 
 // Wait until this wave's vector-memory operations (including LDS DMA) have completed.
 __device__ inline void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+// Wait until at most N of this wave's vector-memory operations are outstanding (they complete in
+// issue order, so everything issued before the last N has landed). gfx9 encoding: vmcnt in bits
+// 3:0 and 15:14; expcnt and lgkmcnt left at their maxima.
+template <int N>
+__device__ inline void wait_vmem_keep() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
 
 // The other half-wave's value combined with this lane's: v_permlane32_swap exchanges the two
 // 32-lane halves, and its two results hold this lane's value and its partner's (lane ^ 32).
@@ -414,39 +422,40 @@ __global__ __launch_bounds__(256) void fa_bwd_pre_kernel(const u16* __restrict__
 }
 
 // ------------------------------------------------------------------------------------------
-// Backward, dK / dV. Block = 8 waves = 4 groups of 2 waves. A group's two waves own 32 keys
-// each of a 64-key block ("unit") and keep K, V (B operands) and their dK^T, dV^T accumulators
-// in registers. The 4 groups split the unit's (query head, 64-row query tile) iterations
-// round-robin, each streaming its own Q / dO tiles through LDS by DMA, so every KV head's
-// gradient is summed over its H/KVH query heads without repeating K or V. At the end of a unit
-// the 4 partial dK / dV are summed through LDS and stored once in the output dtype (no atomics,
-// no fp32 round trip through HBM). A block takes unit j and unit nkb-1-j, so every block
-// carries the same causal work. Per tile:
+// Backward, dK / dV. Block = 4 waves, one per SIMD, and one block per CU, so each wave has the
+// SIMD's whole register file (up to 512 registers). The block owns a 64-key block ("unit"); every
+// wave holds all 64 keys: K and V as B operands and its own partial dK^T, dV^T accumulators.
+// The 4 waves split the unit's (query head, 64-row query tile) iterations round-robin and each
+// streams its own Q / dO tiles and -lse/scale, -D vectors through a private double-buffered LDS
+// slot by DMA, so the loop needs no block barrier, and every Q / dO operand read from LDS feeds
+// both 32-key slabs. The GQA sum over the H/KVH query heads of a KV head happens in the
+// accumulators. At the end of a unit the 4 partial dK / dV are summed through LDS and stored once
+// in the output dtype (no atomics, no fp32 round trip through HBM). A block takes unit j and unit
+// nkb-1-j, so every block carries the same causal work. Per 32-query step and 32-key slab:
 //   S' = Q K^T - lse/scale, dP' = dO V^T - D   (A = Q / dO rows from LDS, B = K / V registers;
 //                                              the accumulators start from -lse/scale and -D)
 //   P = exp2(S' * sl2), dS = P dP'
 //   dV^T += dO^T P, dK^T += Q^T dS             (A = columns of the Q / dO tiles, B = P / dS registers)
-// Every LDS read of a 32-query step is issued before its products, so the MFMAs do not wait on
-// LDS one by one.
 // ------------------------------------------------------------------------------------------
 template <int HD, int DT>
-__global__ __launch_bounds__(512, 1) void fa_bwd_dkdv_kernel(
+__global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(
     const u16* __restrict__ Q, const u16* __restrict__ K, const u16* __restrict__ V, const u16* __restrict__ dO,
     const float* __restrict__ nLvec, const float* __restrict__ nDvec, u16* __restrict__ dK, u16* __restrict__ dV,
     int BKV, int H, int KVH, int T, int nkb, int nqt, float sl2, float scale) {
     using E = Elem<DT>;
-    constexpr int BNK = 64, BM = 64, NG = 4, GW = 2;
+    constexpr int BNK = 64, BM = 64, NW = 4, NSL = BNK / 32;
     constexpr int NS = HD / 16;
     constexpr int ND = HD / 32;
     constexpr int QT = BM * HD;  // elements of one Q or dO tile
     constexpr int CH4 = HD / 4;  // 16-byte fp32 chunks per staged gradient row
     static_assert(BNK == BM, "a unit's first query tile is its own index");
-    __shared__ __attribute__((aligned(16))) u16 qA[NG * QT];
-    __shared__ __attribute__((aligned(16))) u16 oA[NG * QT];
-    __shared__ __attribute__((aligned(16))) u16 qB[NG * QT];
-    __shared__ __attribute__((aligned(16))) u16 oB[NG * QT];
-    __shared__ __attribute__((aligned(16))) float lA[NG * 2 * BM];  // per group: -lse/scale | -D
-    __shared__ __attribute__((aligned(16))) float lB[NG * 2 * BM];
+    static_assert(2 * NW * QT * 2 * 2 >= NW * 2 * BNK * HD * 4, "gradient staging fits in the tile space");
+    __shared__ __attribute__((aligned(16))) u16 qA[NW * QT];
+    __shared__ __attribute__((aligned(16))) u16 oA[NW * QT];
+    __shared__ __attribute__((aligned(16))) u16 qB[NW * QT];
+    __shared__ __attribute__((aligned(16))) u16 oB[NW * QT];
+    __shared__ __attribute__((aligned(16))) float lA[NW * 2 * BM];  // per wave: -lse/scale | -D
+    __shared__ __attribute__((aligned(16))) float lB[NW * 2 * BM];
 
     const int bid = blockIdx.x;
     const int bk = bid % BKV;
@@ -454,7 +463,6 @@ __global__ __launch_bounds__(512, 1) void fa_bwd_dkdv_kernel(
     const int b = bk / KVH, kvh = bk - b * KVH, group = H / KVH;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
     const int g16 = (lane >> 4) & 1;
-    const int gi = wave >> 1, wk = wave & 1, gtid = tid & (64 * GW - 1);
     const size_t kvoff = (size_t)bk * T * HD;
 
     int qroff[NS], qcoff[ND][2];
@@ -468,161 +476,211 @@ __global__ __launch_bounds__(512, 1) void fa_bwd_dkdv_kernel(
     for (int ui = 0; ui < 2; ++ui) {
         const int unit = ui == 0 ? pj : nkb - 1 - pj;
         if (ui == 1 && unit <= pj) break;  // an odd unit count leaves the middle unit alone
-        const int kb0 = unit * BNK, kw = kb0 + 32 * wk, key = kw + l32;
+        const int kb0 = unit * BNK;
         const int qt_first = unit, nq = nqt - qt_first, niter = group * nq;
-        const int rounds = (niter + NG - 1) / NG;
+        const int nmine = wave < niter ? (niter - wave + NW - 1) / NW : 0;  // iterations wave, wave+NW, ...
 
-        u16x8 kf[NS], vf[NS];
+        u16x8 kf[NSL][NS], vf[NSL][NS];
 #pragma unroll
-        for (int s = 0; s < NS; ++s) {
-            kf[s] = key < T ? ld8(K + kvoff + (size_t)key * HD + 16 * s + 8 * hh) : u16x8{};
-            vf[s] = key < T ? ld8(V + kvoff + (size_t)key * HD + 16 * s + 8 * hh) : u16x8{};
+        for (int sl = 0; sl < NSL; ++sl) {
+            const int key = min(kb0 + 32 * sl + l32, T - 1);  // keys past T are masked below
+#pragma unroll
+            for (int s = 0; s < NS; ++s) {
+                kf[sl][s] = ld8(K + kvoff + (size_t)key * HD + 16 * s + 8 * hh);
+                vf[sl][s] = ld8(V + kvoff + (size_t)key * HD + 16 * s + 8 * hh);
+            }
         }
-        f32x16 dk[ND], dv[ND];
+        f32x16 dk[NSL][ND], dv[NSL][ND];
 #pragma unroll
-        for (int dt = 0; dt < ND; ++dt) dk[dt] = dv[dt] = f32x16{};
+        for (int sl = 0; sl < NSL; ++sl)
+#pragma unroll
+            for (int dt = 0; dt < ND; ++dt) dk[sl][dt] = dv[sl][dt] = f32x16{};
 
-        float lse_r = 0.f, d_r = 0.f;
-        // Fetch iteration itn's Q / dO rows into this group's slot (the group's two waves DMA).
-        auto issue = [&](int itn, u16* qs, u16* os) {
-            const int g = itn / nq, qt = qt_first + itn - g * nq;
-            const int hq = kvh * group + g;
-            const size_t qoff = ((size_t)b * H + hq) * T * HD;
-            dma_rows<HD, BM, GW>(Q + qoff, qt * BM, T, qs + gi * QT, wk, lane);
-            dma_rows<HD, BM, GW>(dO + qoff, qt * BM, T, os + gi * QT, wk, lane);
-            const int q = min(qt * BM + (gtid & (BM - 1)), T - 1);
-            const size_t ro = ((size_t)b * H + hq) * T + q;
-            if (gtid < BM) lse_r = nLvec[ro];
-            else d_r = nDvec[ro];
+        // Iteration itn -> (query head of the group, 64-row query tile).
+        auto qbase_of = [&](int itn) { return (qt_first + itn % nq) * BM; };
+        auto rowoff_of = [&](int itn) { return ((size_t)b * H + kvh * group + itn / nq) * T; };
+        // DMA iteration itn's Q / dO tiles and -lse/scale, -D vectors into this wave's slot.
+        auto issue = [&](int itn, u16* qs, u16* os, float* ls) {
+            const size_t ro = rowoff_of(itn);
+            const int q0 = qbase_of(itn);
+            dma_rows<HD, BM, 1>(Q + ro * HD, q0, T, qs + wave * QT, 0, lane);
+            dma_rows<HD, BM, 1>(dO + ro * HD, q0, T, os + wave * QT, 0, lane);
+            const size_t r = ro + min(q0 + lane, T - 1);
+            __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(nLvec + r), LDS_AS(void, ls + wave * 2 * BM), 4, 0, 0);
+            __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(nDvec + r), LDS_AS(void, ls + wave * 2 * BM + BM), 4, 0, 0);
         };
+        // One 64-query iteration: two 32-query steps, each against both 32-key slabs.
+        // MASK: the iteration crosses the diagonal or T (a separate instantiation, so that unmasked
+        // iterations carry no per-element selects).
+        // Operands of one 32-query step: Q / dO rows (A operands) and -lse/scale, -D as the
+        // accumulators' initial values (element i: query 32qh + (i/4)*8 + 4hh + i%4, the same for
+        // every key); and the Q^T / dO^T columns of its two 16-query chunks.
+        struct RowOps {
+            u16x8 qa[NS], oa[NS];
+            f32x16 s0, d0;
+        };
+        struct ColOps {
+            u16x8 gcol[2][ND], qcol[2][ND];
+        };
+        auto load_rows = [&](int qh, const u16* qb_, const u16* ob_, const float* lb_, RowOps& r) {
+#pragma unroll
+            for (int ks = 0; ks < NS; ++ks) {
+                r.qa[ks] = ld8(qb_ + 32 * qh * HD + qroff[ks]);
+                r.oa[ks] = ld8(ob_ + 32 * qh * HD + qroff[ks]);
+            }
+            const f32x4* lv = reinterpret_cast<const f32x4*>(lb_ + 32 * qh + 4 * hh);
+            const f32x4* dv4 = reinterpret_cast<const f32x4*>(lb_ + BM + 32 * qh + 4 * hh);
+            r.s0 = cat16(lv[0], lv[2], lv[4], lv[6]);  // +8 floats per group of 4 rows
+            r.d0 = cat16(dv4[0], dv4[2], dv4[4], dv4[6]);
+        };
+        auto load_cols = [&](int qh, const u16* qb_, const u16* ob_, ColOps& c) {
+#pragma unroll
+            for (int half = 0; half < 2; ++half) {
+                const u16* oc = ob_ + 16 * (2 * qh + half) * HD;
+                const u16* qc = qb_ + 16 * (2 * qh + half) * HD;
+#pragma unroll
+                for (int dt = 0; dt < ND; ++dt) {
+                    c.gcol[half][dt] = cat4(ld_tr(oc + qcoff[dt][0]), ld_tr(oc + qcoff[dt][1]));
+                    c.qcol[half][dt] = cat4(ld_tr(qc + qcoff[dt][0]), ld_tr(qc + qcoff[dt][1]));
+                }
+            }
+        };
+        // One 64-query iteration: two 32-query steps, each against both 32-key slabs. The second
+        // step's operands are read from LDS while the first step's products run.
         // MASK: the iteration crosses the diagonal or T (a separate instantiation, so that unmasked
         // iterations carry no per-element selects).
         auto compute = [&](auto mask_tag, int qbase, const u16* qs, const u16* os, const float* ls) {
             constexpr bool MASK = decltype(mask_tag)::value;
-            const u16* qb_ = qs + gi * QT;
-            const u16* ob_ = os + gi * QT;
-            const float* lb_ = ls + gi * 2 * BM;
-            const int qlim = key - qbase - 4 * hh;  // query offsets below this are in the future of the key
-#pragma unroll 1
+            const u16* qb_ = qs + wave * QT;
+            const u16* ob_ = os + wave * QT;
+            const float* lb_ = ls + wave * 2 * BM;
+            RowOps r[2];
+            ColOps c[2];
+            load_rows(0, qb_, ob_, lb_, r[0]);
+            load_cols(0, qb_, ob_, c[0]);
+#pragma unroll
             for (int qh = 0; qh < 2; ++qh) {
-                const u16* qrow = qb_ + 32 * qh * HD;
-                const u16* orow = ob_ + 32 * qh * HD;
-                const float* lq = lb_ + 32 * qh + 4 * hh;
-                // All LDS reads of this 32-query step first: Q / dO rows, -lse/scale and -D as the
-                // accumulators' initial values (element i: query 32qh + (i/4)*8 + 4hh + i%4), and
-                // the Q^T / dO^T columns of both 16-query chunks.
-                u16x8 qa[NS], oa[NS];
+                f32x16 s[NSL], dp[NSL];
 #pragma unroll
-                for (int ks = 0; ks < NS; ++ks) {
-                    qa[ks] = ld8(qrow + qroff[ks]);
-                    oa[ks] = ld8(orow + qroff[ks]);
-                }
-                const f32x4* lv = reinterpret_cast<const f32x4*>(lq);
-                const f32x4* dv4 = reinterpret_cast<const f32x4*>(lq + BM);
-                f32x16 s = cat16(lv[0], lv[2], lv[4], lv[6]);    // +8 floats per group of 4 rows
-                f32x16 dp = cat16(dv4[0], dv4[2], dv4[4], dv4[6]);
-                u16x8 gcol[2][ND], qcol[2][ND];
-                auto load_cols = [&](int half) {
-                    const u16* oc = ob_ + 16 * (2 * qh + half) * HD;
-                    const u16* qc = qb_ + 16 * (2 * qh + half) * HD;
+                for (int sl = 0; sl < NSL; ++sl) {
+                    s[sl] = r[qh].s0;
+                    dp[sl] = r[qh].d0;
 #pragma unroll
-                    for (int dt = 0; dt < ND; ++dt) {
-                        gcol[half][dt] = cat4(ld_tr(oc + qcoff[dt][0]), ld_tr(oc + qcoff[dt][1]));
-                        qcol[half][dt] = cat4(ld_tr(qc + qcoff[dt][0]), ld_tr(qc + qcoff[dt][1]));
+                    for (int ks = 0; ks < NS; ++ks) {
+                        s[sl] = E::mfma(r[qh].qa[ks], kf[sl][ks], s[sl]);
+                        dp[sl] = E::mfma(r[qh].oa[ks], vf[sl][ks], dp[sl]);
                     }
-                };
-                load_cols(0);
-#pragma unroll
-                for (int ks = 0; ks < NS; ++ks) {
-                    s = E::mfma(qa[ks], kf[ks], s);
-                    dp = E::mfma(oa[ks], vf[ks], dp);
                 }
-                load_cols(1);  // in flight while the softmax runs
-#pragma unroll
-                for (int i = 0; i < 16; ++i) {
-                    const float p = fast_exp2(s[i] * sl2);
-                    dp[i] *= p;
-                    s[i] = p;
+                if (qh == 0) {
+                    load_rows(1, qb_, ob_, lb_, r[1]);
+                    load_cols(1, qb_, ob_, c[1]);
                 }
-                if (MASK) {  // visible iff key <= q, q < T and key < T
-                    const int qrem = T - qbase - 32 * qh - 4 * hh;  // query offsets >= this are past T
-                    const bool kin = key < T;
+#pragma unroll
+                for (int sl = 0; sl < NSL; ++sl) {
 #pragma unroll
                     for (int i = 0; i < 16; ++i) {
-                        const int qo = 32 * qh + (i >> 2) * 8 + (i & 3);
-                        const bool keep = (qo >= qlim) & ((i >> 2) * 8 + (i & 3) < qrem) & kin;
-                        s[i] = keep ? s[i] : 0.f;
-                        dp[i] = keep ? dp[i] : 0.f;
+                        const float p = fast_exp2(s[sl][i] * sl2);
+                        dp[sl][i] *= p;
+                        s[sl][i] = p;
                     }
-                }
+                    if (MASK) {  // visible iff key <= q, q < T and key < T
+                        const int key = kb0 + 32 * sl + l32;
+                        const int qlo = key - qbase - 32 * qh - 4 * hh;  // offsets below this: future
+                        const int qhi = T - qbase - 32 * qh - 4 * hh;    // offsets at or above this: past T
+                        const bool kin = key < T;
 #pragma unroll
-                for (int half = 0; half < 2; ++half) {
-                    // 16-query chunk 2qh + half: queries 16(2qh+half) + (j/4)*8 + 4hh + j%4
-                    const u16x8 pf = pack8<DT>(s, 8 * half);
-                    const u16x8 sf = pack8<DT>(dp, 8 * half);
+                        for (int i = 0; i < 16; ++i) {
+                            const int qo = (i >> 2) * 8 + (i & 3);
+                            const bool keep = (qo >= qlo) & (qo < qhi) & kin;
+                            s[sl][i] = keep ? s[sl][i] : 0.f;
+                            dp[sl][i] = keep ? dp[sl][i] : 0.f;
+                        }
+                    }
 #pragma unroll
-                    for (int dt = 0; dt < ND; ++dt) {
-                        dv[dt] = E::mfma(gcol[half][dt], pf, dv[dt]);
-                        dk[dt] = E::mfma(qcol[half][dt], sf, dk[dt]);
+                    for (int half = 0; half < 2; ++half) {
+                        // 16-query chunk 2qh + half: queries 16(2qh+half) + (j/4)*8 + 4hh + j%4
+                        const u16x8 pf = pack8<DT>(s[sl], 8 * half);
+                        const u16x8 sf = pack8<DT>(dp[sl], 8 * half);
+#pragma unroll
+                        for (int dt = 0; dt < ND; ++dt) {
+                            dv[sl][dt] = E::mfma(c[qh].gcol[half][dt], pf, dv[sl][dt]);
+                            dk[sl][dt] = E::mfma(c[qh].qcol[half][dt], sf, dk[sl][dt]);
+                        }
                     }
                 }
             }
         };
-        // Round r: group gi computes iteration NG*r + gi while fetching NG*(r+1) + gi.
-        auto round = [&](int r, const u16* qs, const u16* os, const float* ls, u16* qn, u16* on, float* ln) {
-            const int itn = NG * r + gi, nxt = itn + NG;
-            __syncthreads();
-            if (nxt < niter) issue(nxt, qn, on);
-            if (itn < niter) {
-                const int g = itn / nq, qbase = (qt_first + itn - g * nq) * BM;
-                if (kw <= qbase + BM - 1 && kw < T) {  // else every key of this wave is in the future
-                    if ((kw + 31 > qbase) || (qbase + BM > T) || (kw + 32 > T))
-                        compute(std::true_type{}, qbase, qs, os, ls);
-                    else
-                        compute(std::false_type{}, qbase, qs, os, ls);
-                }
-            }
-            wait_vmem();
-            if (nxt < niter) ln[gi * 2 * BM + gtid] = gtid < BM ? lse_r : d_r;
+        auto run = [&](int itn, const u16* qs, const u16* os, const float* ls) {
+            const int qbase = qbase_of(itn);
+            if ((kb0 + BNK - 1 > qbase) || (qbase + BM > T) || (kb0 + BNK > T))
+                compute(std::true_type{}, qbase, qs, os, ls);
+            else
+                compute(std::false_type{}, qbase, qs, os, ls);
         };
-
-        if (gi < niter) issue(gi, qA, oA);
-        wait_vmem();
-        if (gi < niter) lA[gi * 2 * BM + gtid] = gtid < BM ? lse_r : d_r;
-        for (int r = 0; r < rounds; r += 2) {
-            round(r, qA, oA, lA, qB, oB, lB);
-            if (r + 1 >= rounds) break;
-            round(r + 1, qB, oB, lB, qA, oA, lA);
+        // Double-buffered: this wave's iteration j uses buffer j % 2 while j + 1 streams into the other.
+        // The DMA into a buffer is issued only after this wave's own reads of it (iteration j - 1)
+        // have returned, which their use by the MFMAs guarantees.
+        constexpr int kDmaOps = 2 * (QT / 8 / 64) + 2;  // vector-memory instructions per issue()
+        if (nmine > 0) issue(wave, qA, oA, lA);
+        for (int j = 0; j < nmine; j += 2) {
+            const int itn = wave + NW * j;
+            if (j + 1 < nmine) {
+                issue(itn + NW, qB, oB, lB);
+                wait_vmem_keep<kDmaOps>();
+            } else {
+                wait_vmem();
+            }
+            run(itn, qA, oA, lA);
+            if (j + 1 >= nmine) break;
+            if (j + 2 < nmine) {
+                issue(itn + 2 * NW, qA, oA, lA);
+                wait_vmem_keep<kDmaOps>();
+            } else {
+                wait_vmem();
+            }
+            run(itn + NW, qB, oB, lB);
         }
 
-        // Sum the groups' partial dK^T / dV^T (lane = key, element i = column
-        // 32dt + (i/4)*8 + 4hh + i%4) through LDS: [64 keys][HD] fp32 per (tensor, group), 16-byte
+        // Sum the 4 waves' partial dK^T / dV^T (lane = key, element i = column
+        // 32dt + (i/4)*8 + 4hh + i%4) through LDS: [64 keys][HD] fp32 per (tensor, wave), 16-byte
         // chunks XOR-swizzled by row.
         __syncthreads();
-        float* sk = reinterpret_cast<float*>(gi < 2 ? qA : oA) + (gi & 1) * BNK * HD;
-        float* sv = reinterpret_cast<float*>(gi < 2 ? qB : oB) + (gi & 1) * BNK * HD;
-        const int kr = 32 * wk + l32;
+        // The epilogue's addressing is derived from a copy of tid the compiler cannot see through,
+        // so it is computed here rather than hoisted to the kernel entry and spilled across the loop.
+        int etid;
+        __asm__ volatile("v_mov_b32 %0, %1" : "=v"(etid) : "v"(tid));
+        float* stage = reinterpret_cast<float*>(wave < 2 ? (wave == 0 ? qA : oA) : (wave == 2 ? qB : oB));
+        float* sk = stage;
+        float* sv = stage + BNK * HD;
 #pragma unroll
-        for (int dt = 0; dt < ND; ++dt)
+        for (int sl = 0; sl < NSL; ++sl) {
+            const int kr = 32 * sl + l32;
 #pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                const int cc = ((8 * dt + 2 * g + hh) ^ kr) & (CH4 - 1);
-                *reinterpret_cast<f32x4*>(sk + kr * HD + 4 * cc) = f32x4{dk[dt][4 * g], dk[dt][4 * g + 1], dk[dt][4 * g + 2], dk[dt][4 * g + 3]};
-                *reinterpret_cast<f32x4*>(sv + kr * HD + 4 * cc) = f32x4{dv[dt][4 * g], dv[dt][4 * g + 1], dv[dt][4 * g + 2], dv[dt][4 * g + 3]};
-            }
+            for (int dt = 0; dt < ND; ++dt)
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const int cc = ((8 * dt + 2 * g + hh) ^ kr) & (CH4 - 1);
+                    *reinterpret_cast<f32x4*>(sk + kr * HD + 4 * cc) =
+                        f32x4{dk[sl][dt][4 * g], dk[sl][dt][4 * g + 1], dk[sl][dt][4 * g + 2], dk[sl][dt][4 * g + 3]};
+                    *reinterpret_cast<f32x4*>(sv + kr * HD + 4 * cc) =
+                        f32x4{dv[sl][dt][4 * g], dv[sl][dt][4 * g + 1], dv[sl][dt][4 * g + 2], dv[sl][dt][4 * g + 3]};
+                }
+        }
         __syncthreads();
+        const float* st0 = reinterpret_cast<const float*>(qA);
+        const float* st1 = reinterpret_cast<const float*>(oA);
+        const float* st2 = reinterpret_cast<const float*>(qB);
+        const float* st3 = reinterpret_cast<const float*>(oB);
 #pragma unroll
-        for (int k = 0; k < 2 * BNK * CH4 / 512; ++k) {
-            const int it = tid + 512 * k;
+        for (int k = 0; k < 2 * BNK * CH4 / 256; ++k) {
+            const int it = etid + 256 * k;
             const int which = it / (BNK * CH4), rem = it - which * (BNK * CH4);
             const int row = rem / CH4, c = rem - row * CH4;
-            const int off = row * HD + 4 * ((c ^ row) & (CH4 - 1));
-            const float* s0 = which == 0 ? reinterpret_cast<const float*>(qA) : reinterpret_cast<const float*>(qB);
-            const float* s1 = which == 0 ? reinterpret_cast<const float*>(oA) : reinterpret_cast<const float*>(oB);
-            f32x4 acc = *reinterpret_cast<const f32x4*>(s0 + off);
-            acc += *reinterpret_cast<const f32x4*>(s0 + BNK * HD + off);
-            acc += *reinterpret_cast<const f32x4*>(s1 + off);
-            acc += *reinterpret_cast<const f32x4*>(s1 + BNK * HD + off);
+            const int off = which * BNK * HD + row * HD + 4 * ((c ^ row) & (CH4 - 1));
+            f32x4 acc = *reinterpret_cast<const f32x4*>(st0 + off);
+            acc += *reinterpret_cast<const f32x4*>(st1 + off);
+            acc += *reinterpret_cast<const f32x4*>(st2 + off);
+            acc += *reinterpret_cast<const f32x4*>(st3 + off);
             if (which == 0) acc *= scale;
             if (kb0 + row < T) {
                 u16* dst = (which == 0 ? dK : dV) + kvoff + (size_t)(kb0 + row) * HD + 4 * c;
@@ -862,7 +920,7 @@ int dkdv_impl(const void* q, const void* k, const void* v, const void* dO, const
     const int nqt = nkb;                   // 64-row query tiles
     const int npairs = (nkb + 1) / 2;
     const int BKV = (int)(B * KVH);
-    fa_bwd_dkdv_kernel<HD, DT><<<dim3(npairs * BKV), dim3(512), 0, st>>>(
+    fa_bwd_dkdv_kernel<HD, DT><<<dim3(npairs * BKV), dim3(256), 0, st>>>(
         (const u16*)q, (const u16*)k, (const u16*)v, (const u16*)dO, w.nL, w.nD, (u16*)dk, (u16*)dv, BKV, (int)H,
         (int)KVH, (int)T, nkb, nqt, scale * kLog2e, scale);
     return launch_status("fa_bwd_dkdv_kernel");
