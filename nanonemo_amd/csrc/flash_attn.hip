@@ -164,21 +164,42 @@ __device__ inline u16x4 ld_tr(const u16* p) {
     return __builtin_bit_cast(u16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16(LDS_AS(s16x4, const_cast<u16*>(p))));
 }
 
+// Per-lane part of the DMA addressing of a W-column tile (computed once per kernel): the byte
+// offset of the lane's row within one copy instruction (a copy instruction moves 64 chunks of 16
+// bytes, i.e. 64 / (W / 8) rows), and the lane's swizzled chunk byte offset. An instruction's rows
+// start at a multiple of 64 / (W / 8); the swizzle reads row bits 1..3 (W = 64), of which that
+// start contributes only bit 3 (cB1 applies to odd instructions), or bits 2..3 (W = 32), which it
+// never touches.
+struct DmaLane {
+    uint32_t rowB, cB0, cB1;
+};
+template <int W>
+__device__ inline DmaLane dma_lane(int lane) {
+    constexpr int CH = W / 8;
+    const int rl = lane / CH, cl = lane % CH;
+    return {(uint32_t)rl * (W * 2), (uint32_t)swz_chunk<W>(rl, cl) * 16, (uint32_t)swz_chunk<W>(rl + 8, cl) * 16};
+}
+
 // Copies rows [r0, r0 + ROWS) of a row-major [T][W] global matrix (rows past T - 1 repeat row
 // T - 1; their results are masked by the callers) into a swizzled LDS tile, 16 bytes per lane.
+// `g`, `r0`, `T`, `lds` and `wave` are wave-uniform: each copy instruction addresses a uniform
+// tile base plus a 32-bit per-lane byte offset, and its LDS destination is the uniform base +
+// 16 * lane. The per-lane terms are re-derived from `dl` at each call rather than kept per
+// instruction across the caller's loop.
 template <int W, int ROWS, int NW>
-__device__ inline void dma_rows(const u16* __restrict__ g, int r0, int T, u16* lds, int wave, int lane) {
+__device__ inline void dma_rows(const u16* __restrict__ g, int r0, int T, u16* lds, int wave, DmaLane dl) {
     constexpr int CH = W / 8, NCH = ROWS * CH;
-    static_assert(NCH % (64 * NW) == 0, "tile must split evenly over the block's waves");
+    static_assert(NCH % (64 * NW) == 0 && 64 % CH == 0, "tile must split evenly over the block's waves");
+    __asm__ volatile("" : "+v"(dl.rowB), "+v"(dl.cB0), "+v"(dl.cB1));
+    const char* gt = reinterpret_cast<const char*>(g + (size_t)r0 * W);
+    const uint32_t limB = (uint32_t)min(T - 1 - r0, ROWS - 1) * (W * 2);
 #pragma unroll
     for (int it = 0; it < NCH / (64 * NW); ++it) {
-        const int p0 = (it * NW + wave) * 64;  // first chunk written by this wave instruction
-        const int p = p0 + lane;
-        const int row = p / CH;
-        const int c = swz_chunk<W>(row, p % CH);
-        const int gr = min(r0 + row, T - 1);
-        __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(g + (size_t)gr * W + c * 8),
-                                         LDS_AS(void, lds + p0 * 8), 16, 0, 0);
+        const int k = it * NW + wave;  // copy instruction index within the tile
+        const uint32_t rb = dl.rowB + (uint32_t)(k * (64 / CH) * (W * 2));
+        const uint32_t cb = (W == 64 && (k & 1)) ? dl.cB1 : dl.cB0;
+        __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(gt + (min(rb, limB) + cb)),
+                                         LDS_AS(void, lds + k * 64 * 8), 16, 0, 0);
     }
 }
 
@@ -240,7 +261,9 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_kernel(const u16* __restrict__ 
     const u16* Kp = K + kvoff;
     const u16* Vp = V + kvoff;
 
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
+    const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const DmaLane dl = dma_lane<HD>(lane);
     const int g16 = (lane >> 4) & 1;  // which 16-column half of a 32-wide MFMA tile this lane reads
     const int q0 = qb * BM, qw = q0 + wave * 32, qrow = qw + l32;
 
@@ -265,8 +288,8 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_kernel(const u16* __restrict__ 
 
     const int ntiles = (min(q0 + BM, T) + BN - 1) / BN;
     auto issue = [&](int it, u16* kb, u16* vb) {
-        dma_rows<HD, BN, NW>(Kp, it * BN, T, kb, wave, lane);
-        dma_rows<HD, BN, NW>(Vp, it * BN, T, vb, wave, lane);
+        dma_rows<HD, BN, NW>(Kp, it * BN, T, kb, wave, dl);
+        dma_rows<HD, BN, NW>(Vp, it * BN, T, vb, wave, dl);
     };
     // One 128-key tile as four 32-key sub-tiles, software-pipelined so that the matrix unit and the
     // VALU have independent work in the same stretch of straight-line code:
@@ -461,7 +484,9 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(
     const int bk = bid % BKV;
     const int pj = bid / BKV;
     const int b = bk / KVH, kvh = bk - b * KVH, group = H / KVH;
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
+    const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
+    const int wave = tid >> 6;  // a uniform copy in an SGPR costs this kernel more than it saves
+    const DmaLane dl = dma_lane<HD>(lane);
     const int g16 = (lane >> 4) & 1;
     const size_t kvoff = (size_t)bk * T * HD;
 
@@ -501,13 +526,16 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(
         auto rowoff_of = [&](int itn) { return ((size_t)b * H + kvh * group + itn / nq) * T; };
         // DMA iteration itn's Q / dO tiles and -lse/scale, -D vectors into this wave's slot.
         auto issue = [&](int itn, u16* qs, u16* os, float* ls) {
-            const size_t ro = rowoff_of(itn);
-            const int q0 = qbase_of(itn);
-            dma_rows<HD, BM, 1>(Q + ro * HD, q0, T, qs + wave * QT, 0, lane);
-            dma_rows<HD, BM, 1>(dO + ro * HD, q0, T, os + wave * QT, 0, lane);
-            const size_t r = ro + min(q0 + lane, T - 1);
-            __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(nLvec + r), LDS_AS(void, ls + wave * 2 * BM), 4, 0, 0);
-            __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(nDvec + r), LDS_AS(void, ls + wave * 2 * BM + BM), 4, 0, 0);
+            // Wave-uniform in fact; made uniform for the compiler only here, so that the tile
+            // addressing is scalar without keeping scalar copies alive across the whole kernel.
+            const int itu = __builtin_amdgcn_readfirstlane(itn), wu = __builtin_amdgcn_readfirstlane(wave);
+            const size_t ro = rowoff_of(itu);
+            const int q0 = qbase_of(itu);
+            dma_rows<HD, BM, 1>(Q + ro * HD, q0, T, qs + wu * QT, 0, dl);
+            dma_rows<HD, BM, 1>(dO + ro * HD, q0, T, os + wu * QT, 0, dl);
+            const uint32_t lo = (uint32_t)min(lane, T - 1 - q0) * 4;  // rows past T repeat row T - 1
+            __builtin_amdgcn_global_load_lds(reinterpret_cast<const char*>(nLvec + ro + q0) + lo, LDS_AS(void, ls + wu * 2 * BM), 4, 0, 0);
+            __builtin_amdgcn_global_load_lds(reinterpret_cast<const char*>(nDvec + ro + q0) + lo, LDS_AS(void, ls + wu * 2 * BM + BM), 4, 0, 0);
         };
         // One 64-query iteration: two 32-query steps, each against both 32-key slabs.
         // MASK: the iteration crosses the diagonal or T (a separate instantiation, so that unmasked
@@ -727,7 +755,9 @@ __global__ __launch_bounds__(256, 2) void fa_bwd_dq_kernel(const u16* __restrict
     const u16* Kp = K + kvoff;
     const u16* Vp = V + kvoff;
 
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
+    const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const DmaLane dl = dma_lane<HD>(lane);
     const int g16 = (lane >> 4) & 1;
     const int q0 = qb * BM, qw = q0 + wave * 32, qrow = qw + l32;
     const int qc_ = min(qrow, T - 1);
@@ -755,8 +785,8 @@ __global__ __launch_bounds__(256, 2) void fa_bwd_dq_kernel(const u16* __restrict
 
     const int ntiles = (min(q0 + BM, T) + BN - 1) / BN;
     auto issue = [&](int it, u16* kb, u16* vb) {
-        dma_rows<HD, BN, NW>(Kp, it * BN, T, kb, wave, lane);
-        dma_rows<HD, BN, NW>(Vp, it * BN, T, vb, wave, lane);
+        dma_rows<HD, BN, NW>(Kp, it * BN, T, kb, wave, dl);
+        dma_rows<HD, BN, NW>(Vp, it * BN, T, vb, wave, dl);
     };
     // -D enters as the initial value of every dP^T accumulator (the same for all of a lane's keys).
     f32x16 ndv;
