@@ -36,6 +36,19 @@ int nn_fa_fwd(const void* q, const void* k, const void* v, void* o, float* lse,
               int64_t B, int64_t H, int64_t KVH, int64_t T, int64_t D,
               int dtype, float scale, void* stream);
 
+/* Forward on strided views: as nn_fa_fwd, but q and o are read / written through the element
+ * strides qo_strides = {batch, head, row} of a [B, H, T, D] view, and k, v through kv_strides of
+ * a [B, KVH, T, D] view (the D stride is 1 in both). Every stride is a positive multiple of 8
+ * elements and rows are at least D apart. With the (B, T, heads, D) layout that the model's
+ * projections produce ({T*H*D, D, H*D} and {T*KVH*D, D, KVH*D}), q, k and v are consumed and o is
+ * produced in place, so the transposes and .contiguous() copies of
+ * /root/reference/nanonemo/model/layers.py:97-104,116 and
+ * /root/reference/nanonemo/kernels/cuda/flash_attn.py:20 disappear. lse stays dense [B, H, T]. */
+int nn_fa_fwd_strided(const void* q, const void* k, const void* v, void* o, float* lse,
+                      int64_t B, int64_t H, int64_t KVH, int64_t T, int64_t D,
+                      const int64_t qo_strides[3], const int64_t kv_strides[3],
+                      int dtype, float scale, void* stream);
+
 /* Bytes of device workspace the backward needs: -rowsum(dO * o) and -lse / scale, one fp32 each
  * per query row. The caller allocates it, 256-byte aligned; its contents on entry
  * do not matter. */
@@ -52,6 +65,16 @@ int nn_fa_bwd(const void* dO, const void* q, const void* k, const void* v, const
               void* workspace, size_t workspace_bytes,
               int64_t B, int64_t H, int64_t KVH, int64_t T, int64_t D,
               int dtype, float scale, void* stream);
+
+/* Backward on strided views: as nn_fa_bwd, with dO, q, o and dq through qo_strides and k, v, dk
+ * and dv through kv_strides (see nn_fa_fwd_strided). Replaces the .contiguous() copies of
+ * /root/reference/nanonemo/kernels/cuda/flash_attn.py:33 and the transposes of the gradients. */
+int nn_fa_bwd_strided(const void* dO, const void* q, const void* k, const void* v, const void* o,
+                      const float* lse, void* dq, void* dk, void* dv,
+                      void* workspace, size_t workspace_bytes,
+                      int64_t B, int64_t H, int64_t KVH, int64_t T, int64_t D,
+                      const int64_t qo_strides[3], const int64_t kv_strides[3],
+                      int dtype, float scale, void* stream);
 
 /* Backward, stage 1: -D = -rowsum(dO * o) and -lse / scale, fp32, into the workspace.
  * Replaces the ATen preprocessing inside flash_bwd, flash_attn.cu:387-391. */

@@ -164,44 +164,53 @@ __device__ inline u16x4 ld_tr(const u16* p) {
     return __builtin_bit_cast(u16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16(LDS_AS(s16x4, const_cast<u16*>(p))));
 }
 
-// Per-lane part of the DMA addressing of a W-column tile (computed once per kernel): the byte
-// offset of the lane's row within one copy instruction (a copy instruction moves 64 chunks of 16
-// bytes, i.e. 64 / (W / 8) rows), and the lane's swizzled chunk byte offset. An instruction's rows
-// start at a multiple of 64 / (W / 8); the swizzle reads row bits 1..3 (W = 64), of which that
-// start contributes only bit 3 (cB1 applies to odd instructions), or bits 2..3 (W = 32), which it
-// never touches.
+// Per-lane part of the DMA addressing of a W-column tile (computed once per kernel): the lane's
+// row within one copy instruction (a copy instruction moves 64 chunks of 16 bytes, i.e.
+// 64 / (W / 8) rows) and its swizzled chunk byte offset. An instruction's rows start at a
+// multiple of 64 / (W / 8); the swizzle reads row bits 1..3 (W = 64), of which that start
+// contributes only bit 3 (cB1 applies to odd instructions), or bits 2..3 (W = 32), which it never
+// touches.
 struct DmaLane {
-    uint32_t rowB, cB0, cB1;
+    uint32_t rl, cB0, cB1;
 };
 template <int W>
 __device__ inline DmaLane dma_lane(int lane) {
     constexpr int CH = W / 8;
     const int rl = lane / CH, cl = lane % CH;
-    return {(uint32_t)rl * (W * 2), (uint32_t)swz_chunk<W>(rl, cl) * 16, (uint32_t)swz_chunk<W>(rl + 8, cl) * 16};
+    return {(uint32_t)rl, (uint32_t)swz_chunk<W>(rl, cl) * 16, (uint32_t)swz_chunk<W>(rl + 8, cl) * 16};
 }
 
-// Copies rows [r0, r0 + ROWS) of a row-major [T][W] global matrix (rows past T - 1 repeat row
-// T - 1; their results are masked by the callers) into a swizzled LDS tile, 16 bytes per lane.
-// `g`, `r0`, `T`, `lds` and `wave` are wave-uniform: each copy instruction addresses a uniform
-// tile base plus a 32-bit per-lane byte offset, and its LDS destination is the uniform base +
-// 16 * lane. The per-lane terms are re-derived from `dl` at each call rather than kept per
-// instruction across the caller's loop.
+// Copies rows [r0, r0 + ROWS) of a [T][W] global matrix with row stride `ld` elements (rows past
+// T - 1 repeat row T - 1; their results are masked by the callers) into a swizzled row-major LDS
+// tile, 16 bytes per lane. `g`, `ld`, `r0`, `T`, `lds` and `wave` are wave-uniform: each copy
+// instruction addresses a uniform tile base plus a 32-bit per-lane byte offset, and its LDS
+// destination is the uniform base + 16 * lane. The per-lane terms are re-derived from `dl` at
+// each call rather than kept per instruction across the caller's loop.
 template <int W, int ROWS, int NW>
-__device__ inline void dma_rows(const u16* __restrict__ g, int r0, int T, u16* lds, int wave, DmaLane dl) {
+__device__ inline void dma_rows(const u16* __restrict__ g, int ld, int r0, int T, u16* lds, int wave, DmaLane dl) {
     constexpr int CH = W / 8, NCH = ROWS * CH;
     static_assert(NCH % (64 * NW) == 0 && 64 % CH == 0, "tile must split evenly over the block's waves");
-    __asm__ volatile("" : "+v"(dl.rowB), "+v"(dl.cB0), "+v"(dl.cB1));
-    const char* gt = reinterpret_cast<const char*>(g + (size_t)r0 * W);
-    const uint32_t limB = (uint32_t)min(T - 1 - r0, ROWS - 1) * (W * 2);
+    __asm__ volatile("" : "+v"(dl.rl), "+v"(dl.cB0), "+v"(dl.cB1));
+    const char* gt = reinterpret_cast<const char*>(g + (size_t)r0 * ld);
+    const uint32_t ldB = (uint32_t)ld * 2;
+    const uint32_t limB = (uint32_t)min(T - 1 - r0, ROWS - 1) * ldB;
 #pragma unroll
     for (int it = 0; it < NCH / (64 * NW); ++it) {
         const int k = it * NW + wave;  // copy instruction index within the tile
-        const uint32_t rb = dl.rowB + (uint32_t)(k * (64 / CH) * (W * 2));
+        const uint32_t rb = (dl.rl + (uint32_t)(k * (64 / CH))) * ldB;
         const uint32_t cb = (W == 64 && (k & 1)) ? dl.cB1 : dl.cB0;
         __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(gt + (min(rb, limB) + cb)),
                                          LDS_AS(void, lds + k * 64 * 8), 16, 0, 0);
     }
 }
+
+// Element strides of a [B][heads][T][D] tensor view whose D stride is 1: batch, head and row
+// (sequence position). Q, O, dO and dQ share one layout; K, V, dK and dV another.
+struct Lay {
+    long long sb, sh;
+    int st;
+    __device__ size_t at(int b, int h) const { return (size_t)b * sb + (size_t)h * sh; }
+};
 
 // Wait until this wave's vector-memory operations (including LDS DMA) have completed.
 __device__ inline void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
@@ -238,7 +247,7 @@ template <int HD, int DT>
 __global__ __launch_bounds__(256, 2) void fa_fwd_kernel(const u16* __restrict__ Q, const u16* __restrict__ K,
                                                         const u16* __restrict__ V, u16* __restrict__ O,
                                                         float* __restrict__ LSE, int BH, int H, int KVH, int T,
-                                                        int nqb, float sl2) {
+                                                        int nqb, float sl2, Lay lq, Lay lk) {
     using E = Elem<DT>;
     constexpr int BM = 128, BN = 128, NW = 4;
     constexpr int NS = HD / 16;  // k-steps of Q K^T
@@ -256,8 +265,8 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_kernel(const u16* __restrict__ 
     const int qb = nqb - 1 - bid / BH;
     const int b = bh / H, h = bh - b * H;
     const int kvh = h / (H / KVH);
-    const size_t qoff = (size_t)bh * T * HD;
-    const size_t kvoff = ((size_t)b * KVH + kvh) * T * HD;
+    const size_t qoff = lq.at(b, h);
+    const size_t kvoff = lk.at(b, kvh);
     const u16* Kp = K + kvoff;
     const u16* Vp = V + kvoff;
 
@@ -269,7 +278,7 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_kernel(const u16* __restrict__ 
 
     u16x8 qf[NS];
 #pragma unroll
-    for (int s = 0; s < NS; ++s) qf[s] = qrow < T ? ld8(Q + qoff + (size_t)qrow * HD + 16 * s + 8 * hh) : u16x8{};
+    for (int s = 0; s < NS; ++s) qf[s] = qrow < T ? ld8(Q + qoff + (size_t)qrow * lq.st + 16 * s + 8 * hh) : u16x8{};
 
     f32x16 oacc[ND];
 #pragma unroll
@@ -288,8 +297,8 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_kernel(const u16* __restrict__ 
 
     const int ntiles = (min(q0 + BM, T) + BN - 1) / BN;
     auto issue = [&](int it, u16* kb, u16* vb) {
-        dma_rows<HD, BN, NW>(Kp, it * BN, T, kb, wave, dl);
-        dma_rows<HD, BN, NW>(Vp, it * BN, T, vb, wave, dl);
+        dma_rows<HD, BN, NW>(Kp, lk.st, it * BN, T, kb, wave, dl);
+        dma_rows<HD, BN, NW>(Vp, lk.st, it * BN, T, vb, wave, dl);
     };
     // One 128-key tile as four 32-key sub-tiles, software-pipelined so that the matrix unit and the
     // VALU have independent work in the same stretch of straight-line code:
@@ -403,7 +412,7 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_kernel(const u16* __restrict__ 
     const float ltot = pair_sum(lsum);
     if (qrow < T) {
         const float inv = 1.f / ltot;
-        u16* op = O + qoff + (size_t)qrow * HD;
+        u16* op = O + qoff + (size_t)qrow * lq.st;
 #pragma unroll
         for (int dt = 0; dt < ND; ++dt)
 #pragma unroll
@@ -424,15 +433,19 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_kernel(const u16* __restrict__ 
 template <int HD, int DT>
 __global__ __launch_bounds__(256) void fa_bwd_pre_kernel(const u16* __restrict__ O, const u16* __restrict__ dO,
                                                          const float* __restrict__ LSE, float* __restrict__ nDvec,
-                                                         float* __restrict__ nLvec, int64_t rows, float inv_scale) {
+                                                         float* __restrict__ nLvec, int64_t rows, int H, int T,
+                                                         float inv_scale, Lay lq) {
     using E = Elem<DT>;
     constexpr int TPR = HD / 8;  // threads per row
     const int64_t gtid = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    const int64_t row = gtid / TPR;
+    const int64_t row = gtid / TPR;  // (batch, head, position) in [B][H][T] order
     const int c = (int)(gtid % TPR);
     float acc = 0.f;
     if (row < rows) {
-        const u16x8 o = ld8(O + row * HD + 8 * c), g = ld8(dO + row * HD + 8 * c);
+        const int64_t bh = row / T;
+        const int t = (int)(row - bh * T), b = (int)(bh / H), h = (int)(bh - (int64_t)b * H);
+        const size_t off = lq.at(b, h) + (size_t)t * lq.st + 8 * c;
+        const u16x8 o = ld8(O + off), g = ld8(dO + off);
 #pragma unroll
         for (int j = 0; j < 8; ++j) acc = fmaf(E::to_f32(o[j]), E::to_f32(g[j]), acc);
     }
@@ -464,7 +477,7 @@ template <int HD, int DT>
 __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(
     const u16* __restrict__ Q, const u16* __restrict__ K, const u16* __restrict__ V, const u16* __restrict__ dO,
     const float* __restrict__ nLvec, const float* __restrict__ nDvec, u16* __restrict__ dK, u16* __restrict__ dV,
-    int BKV, int H, int KVH, int T, int nkb, int nqt, float sl2, float scale) {
+    int BKV, int H, int KVH, int T, int nkb, int nqt, float sl2, float scale, Lay lq, Lay lk) {
     using E = Elem<DT>;
     constexpr int BNK = 64, BM = 64, NW = 4, NSL = BNK / 32;
     constexpr int NS = HD / 16;
@@ -488,7 +501,7 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(
     const int wave = tid >> 6;  // a uniform copy in an SGPR costs this kernel more than it saves
     const DmaLane dl = dma_lane<HD>(lane);
     const int g16 = (lane >> 4) & 1;
-    const size_t kvoff = (size_t)bk * T * HD;
+    const size_t kvoff = lk.at(b, kvh);
 
     int qroff[NS], qcoff[ND][2];
 #pragma unroll
@@ -511,8 +524,8 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(
             const int key = min(kb0 + 32 * sl + l32, T - 1);  // keys past T are masked below
 #pragma unroll
             for (int s = 0; s < NS; ++s) {
-                kf[sl][s] = ld8(K + kvoff + (size_t)key * HD + 16 * s + 8 * hh);
-                vf[sl][s] = ld8(V + kvoff + (size_t)key * HD + 16 * s + 8 * hh);
+                kf[sl][s] = ld8(K + kvoff + (size_t)key * lk.st + 16 * s + 8 * hh);
+                vf[sl][s] = ld8(V + kvoff + (size_t)key * lk.st + 16 * s + 8 * hh);
             }
         }
         f32x16 dk[NSL][ND], dv[NSL][ND];
@@ -523,16 +536,18 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(
 
         // Iteration itn -> (query head of the group, 64-row query tile).
         auto qbase_of = [&](int itn) { return (qt_first + itn % nq) * BM; };
-        auto rowoff_of = [&](int itn) { return ((size_t)b * H + kvh * group + itn / nq) * T; };
+        auto head_of = [&](int itn) { return kvh * group + itn / nq; };
         // DMA iteration itn's Q / dO tiles and -lse/scale, -D vectors into this wave's slot.
         auto issue = [&](int itn, u16* qs, u16* os, float* ls) {
             // Wave-uniform in fact; made uniform for the compiler only here, so that the tile
             // addressing is scalar without keeping scalar copies alive across the whole kernel.
             const int itu = __builtin_amdgcn_readfirstlane(itn), wu = __builtin_amdgcn_readfirstlane(wave);
-            const size_t ro = rowoff_of(itu);
+            const int hq = head_of(itu);
+            const size_t ro = ((size_t)b * H + hq) * T;  // first row of the head's [T] vectors
+            const size_t qo = lq.at(b, hq);
             const int q0 = qbase_of(itu);
-            dma_rows<HD, BM, 1>(Q + ro * HD, q0, T, qs + wu * QT, 0, dl);
-            dma_rows<HD, BM, 1>(dO + ro * HD, q0, T, os + wu * QT, 0, dl);
+            dma_rows<HD, BM, 1>(Q + qo, lq.st, q0, T, qs + wu * QT, 0, dl);
+            dma_rows<HD, BM, 1>(dO + qo, lq.st, q0, T, os + wu * QT, 0, dl);
             const uint32_t lo = (uint32_t)min(lane, T - 1 - q0) * 4;  // rows past T repeat row T - 1
             __builtin_amdgcn_global_load_lds(reinterpret_cast<const char*>(nLvec + ro + q0) + lo, LDS_AS(void, ls + wu * 2 * BM), 4, 0, 0);
             __builtin_amdgcn_global_load_lds(reinterpret_cast<const char*>(nDvec + ro + q0) + lo, LDS_AS(void, ls + wu * 2 * BM + BM), 4, 0, 0);
@@ -711,7 +726,7 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(
             acc += *reinterpret_cast<const f32x4*>(st3 + off);
             if (which == 0) acc *= scale;
             if (kb0 + row < T) {
-                u16* dst = (which == 0 ? dK : dV) + kvoff + (size_t)(kb0 + row) * HD + 4 * c;
+                u16* dst = (which == 0 ? dK : dV) + kvoff + (size_t)(kb0 + row) * lk.st + 4 * c;
                 *reinterpret_cast<u32x2*>(dst) = u32x2{E::pack2(acc[0], acc[1]), E::pack2(acc[2], acc[3])};
             }
         }
@@ -733,7 +748,8 @@ __global__ __launch_bounds__(256, 2) void fa_bwd_dq_kernel(const u16* __restrict
                                                            const u16* __restrict__ V, const u16* __restrict__ dO,
                                                            const float* __restrict__ nLvec,
                                                            const float* __restrict__ nDvec, u16* __restrict__ dQ, int BH,
-                                                           int H, int KVH, int T, int nqb, float sl2, float scale) {
+                                                           int H, int KVH, int T, int nqb, float sl2, float scale,
+                                                           Lay lq, Lay lk) {
     using E = Elem<DT>;
     constexpr int BM = 128, BN = 64, NW = 4;
     constexpr int NS = HD / 16;
@@ -750,8 +766,8 @@ __global__ __launch_bounds__(256, 2) void fa_bwd_dq_kernel(const u16* __restrict
     const int qb = nqb - 1 - bid / BH;
     const int b = bh / H, h = bh - b * H;
     const int kvh = h / (H / KVH);
-    const size_t qoff = (size_t)bh * T * HD;
-    const size_t kvoff = ((size_t)b * KVH + kvh) * T * HD;
+    const size_t qoff = lq.at(b, h);
+    const size_t kvoff = lk.at(b, kvh);
     const u16* Kp = K + kvoff;
     const u16* Vp = V + kvoff;
 
@@ -765,8 +781,8 @@ __global__ __launch_bounds__(256, 2) void fa_bwd_dq_kernel(const u16* __restrict
     u16x8 qf[NS], gf[NS];
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
-        qf[s] = ld8(Q + qoff + (size_t)qc_ * HD + 16 * s + 8 * hh);
-        gf[s] = ld8(dO + qoff + (size_t)qc_ * HD + 16 * s + 8 * hh);
+        qf[s] = ld8(Q + qoff + (size_t)qc_ * lq.st + 16 * s + 8 * hh);
+        gf[s] = ld8(dO + qoff + (size_t)qc_ * lq.st + 16 * s + 8 * hh);
     }
     const float nl2 = nLvec[(size_t)bh * T + qc_] * sl2;  // -lse * log2(e)
     const float nd = nDvec[(size_t)bh * T + qc_];
@@ -785,8 +801,8 @@ __global__ __launch_bounds__(256, 2) void fa_bwd_dq_kernel(const u16* __restrict
 
     const int ntiles = (min(q0 + BM, T) + BN - 1) / BN;
     auto issue = [&](int it, u16* kb, u16* vb) {
-        dma_rows<HD, BN, NW>(Kp, it * BN, T, kb, wave, dl);
-        dma_rows<HD, BN, NW>(Vp, it * BN, T, vb, wave, dl);
+        dma_rows<HD, BN, NW>(Kp, lk.st, it * BN, T, kb, wave, dl);
+        dma_rows<HD, BN, NW>(Vp, lk.st, it * BN, T, vb, wave, dl);
     };
     // -D enters as the initial value of every dP^T accumulator (the same for all of a lane's keys).
     f32x16 ndv;
@@ -856,7 +872,7 @@ __global__ __launch_bounds__(256, 2) void fa_bwd_dq_kernel(const u16* __restrict
     }
 
     if (qrow < T) {
-        u16* dst = dQ + qoff + (size_t)qrow * HD;
+        u16* dst = dQ + qoff + (size_t)qrow * lq.st;
 #pragma unroll
         for (int dt = 0; dt < ND; ++dt)
 #pragma unroll
@@ -924,47 +940,65 @@ Workspace carve(void* base, int64_t B, int64_t H, int64_t T) {
 
 template <int HD, int DT>
 int fwd_impl(const void* q, const void* k, const void* v, void* o, float* lse, int64_t B, int64_t H, int64_t KVH,
-             int64_t T, float scale, hipStream_t st) {
+             int64_t T, float scale, Lay lq, Lay lk, hipStream_t st) {
     const int nqb = (int)((T + 127) / 128);
     const int BH = (int)(B * H);
     fa_fwd_kernel<HD, DT><<<dim3(nqb * BH), dim3(256), 0, st>>>(
-        (const u16*)q, (const u16*)k, (const u16*)v, (u16*)o, lse, BH, (int)H, (int)KVH, (int)T, nqb, scale * kLog2e);
+        (const u16*)q, (const u16*)k, (const u16*)v, (u16*)o, lse, BH, (int)H, (int)KVH, (int)T, nqb, scale * kLog2e, lq, lk);
     return launch_status("fa_fwd_kernel");
 }
 
 template <int HD, int DT>
 int pre_impl(const void* o, const void* dO, const float* lse, const Workspace& w, int64_t B, int64_t H, int64_t KVH,
-             int64_t T, float scale, hipStream_t st) {
+             int64_t T, float scale, Lay lq, hipStream_t st) {
     (void)KVH;
     const int64_t rows = B * H * T;
     const int64_t blocks = (rows * (HD / 8) + 255) / 256;
-    fa_bwd_pre_kernel<HD, DT><<<dim3((unsigned)blocks), dim3(256), 0, st>>>((const u16*)o, (const u16*)dO, lse, w.nD,
-                                                                           w.nL, rows, 1.0f / scale);
+    fa_bwd_pre_kernel<HD, DT><<<dim3((unsigned)blocks), dim3(256), 0, st>>>(
+        (const u16*)o, (const u16*)dO, lse, w.nD, w.nL, rows, (int)H, (int)T, 1.0f / scale, lq);
     return launch_status("fa_bwd_pre_kernel");
 }
 
 template <int HD, int DT>
 int dkdv_impl(const void* q, const void* k, const void* v, const void* dO, const Workspace& w, void* dk, void* dv,
-              int64_t B, int64_t H, int64_t KVH, int64_t T, float scale, hipStream_t st) {
+              int64_t B, int64_t H, int64_t KVH, int64_t T, float scale, Lay lq, Lay lk, hipStream_t st) {
     const int nkb = (int)((T + 63) / 64);  // 64-key units
     const int nqt = nkb;                   // 64-row query tiles
     const int npairs = (nkb + 1) / 2;
     const int BKV = (int)(B * KVH);
     fa_bwd_dkdv_kernel<HD, DT><<<dim3(npairs * BKV), dim3(256), 0, st>>>(
         (const u16*)q, (const u16*)k, (const u16*)v, (const u16*)dO, w.nL, w.nD, (u16*)dk, (u16*)dv, BKV, (int)H,
-        (int)KVH, (int)T, nkb, nqt, scale * kLog2e, scale);
+        (int)KVH, (int)T, nkb, nqt, scale * kLog2e, scale, lq, lk);
     return launch_status("fa_bwd_dkdv_kernel");
 }
 
 template <int HD, int DT>
 int dq_impl(const void* q, const void* k, const void* v, const void* dO, const Workspace& w, void* dq, int64_t B,
-            int64_t H, int64_t KVH, int64_t T, float scale, hipStream_t st) {
+            int64_t H, int64_t KVH, int64_t T, float scale, Lay lq, Lay lk, hipStream_t st) {
     const int nqb = (int)((T + 127) / 128);
     const int BH = (int)(B * H);
     fa_bwd_dq_kernel<HD, DT><<<dim3(nqb * BH), dim3(256), 0, st>>>(
         (const u16*)q, (const u16*)k, (const u16*)v, (const u16*)dO, w.nL, w.nD, (u16*)dq, BH, (int)H, (int)KVH,
-        (int)T, nqb, scale * kLog2e, scale);
+        (int)T, nqb, scale * kLog2e, scale, lq, lk);
     return launch_status("fa_bwd_dq_kernel");
+}
+
+// Dense [B][heads][T][D] layout.
+Lay contiguous(int64_t heads, int64_t T, int64_t D) { return Lay{(long long)(heads * T * D), (long long)(T * D), (int)D}; }
+
+// Validates caller-given element strides {batch, head, row} of a [B][heads][T][D] view with unit D
+// stride: every stride a positive multiple of 8 elements (16-byte rows, so tiles move 16 bytes
+// per lane), rows at least D apart, and row offsets inside one (batch, head) slice below 2^30.
+int take_layout(const int64_t* strides, int64_t heads, int64_t T, int64_t D, const char* what, Lay* out) {
+    if (!strides) return fail(-1, "null %s strides", what);
+    const int64_t sb = strides[0], sh = strides[1], st = strides[2];
+    if (sb <= 0 || sh <= 0 || st <= 0 || sb % 8 || sh % 8 || st % 8)
+        return fail(-1, "%s strides must be positive multiples of 8 elements", what);
+    if (st < D) return fail(-1, "%s row stride is smaller than head_dim", what);
+    if (T * st >= ((int64_t)1 << 30) || sb >= ((int64_t)1 << 40) || sh * heads >= ((int64_t)1 << 40))
+        return fail(-1, "%s strides too large", what);
+    *out = Lay{(long long)sb, (long long)sh, (int)st};
+    return 0;
 }
 
 int check_ws(void* workspace, size_t workspace_bytes, int64_t B, int64_t H, int64_t T) {
@@ -986,7 +1020,7 @@ int check_ws(void* workspace, size_t workspace_bytes, int64_t B, int64_t H, int6
 
 NNFA_API const char* nn_fa_last_error(void) { return g_last_error.c_str(); }
 
-NNFA_API int nn_fa_abi_version(void) { return 4; }
+NNFA_API int nn_fa_abi_version(void) { return 5; }
 
 NNFA_API size_t nn_fa_bwd_workspace_size(int64_t B, int64_t H, int64_t KVH, int64_t T, int64_t D) {
     (void)KVH;
@@ -995,63 +1029,150 @@ NNFA_API size_t nn_fa_bwd_workspace_size(int64_t B, int64_t H, int64_t KVH, int6
     return carve(nullptr, B, H, T).bytes;
 }
 
-NNFA_API int nn_fa_fwd(const void* q, const void* k, const void* v, void* o, float* lse, int64_t B, int64_t H,
-                       int64_t KVH, int64_t T, int64_t D, int dtype, float scale, void* stream) {
+namespace {
+
+int fwd_entry(const void* q, const void* k, const void* v, void* o, float* lse, int64_t B, int64_t H, int64_t KVH,
+              int64_t T, int64_t D, int dtype, float scale, const int64_t* qo_strides, const int64_t* kv_strides,
+              void* stream) {
     g_last_error.clear();
     if (int e = check_dims(B, H, KVH, T, D, dtype)) return e;
     if (B == 0 || T == 0) return 0;
     if (!q || !k || !v || !o || !lse) return fail(-1, "null pointer argument");
     if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o)) return fail(-1, "inputs must be 16-byte aligned");
-    return NNFA_DISPATCH(fwd_impl, D, dtype, q, k, v, o, lse, B, H, KVH, T, scale, (hipStream_t)stream);
+    Lay lq = contiguous(H, T, D), lk = contiguous(KVH, T, D);
+    if (qo_strides)
+        if (int e = take_layout(qo_strides, H, T, D, "q/o", &lq)) return e;
+    if (kv_strides)
+        if (int e = take_layout(kv_strides, KVH, T, D, "k/v", &lk)) return e;
+    return NNFA_DISPATCH(fwd_impl, D, dtype, q, k, v, o, lse, B, H, KVH, T, scale, lq, lk, (hipStream_t)stream);
+}
+
+// Shared argument checks of the backward stages; fills the workspace view and the two layouts.
+int bwd_prologue(const void* workspace, size_t workspace_bytes, int64_t B, int64_t H, int64_t KVH, int64_t T,
+                 int64_t D, int dtype, const int64_t* qo_strides, const int64_t* kv_strides, Workspace* w, Lay* lq,
+                 Lay* lk) {
+    g_last_error.clear();
+    if (int e = check_dims(B, H, KVH, T, D, dtype)) return e;
+    if (B == 0 || T == 0) return 1;  // nothing to do
+    if (int e = check_ws((void*)workspace, workspace_bytes, B, H, T)) return e;
+    *w = carve((void*)workspace, B, H, T);
+    *lq = contiguous(H, T, D);
+    *lk = contiguous(KVH, T, D);
+    if (qo_strides)
+        if (int e = take_layout(qo_strides, H, T, D, "q/o", lq)) return e;
+    if (kv_strides)
+        if (int e = take_layout(kv_strides, KVH, T, D, "k/v", lk)) return e;
+    return 0;
+}
+
+int pre_entry(const void* o, const void* dO, const float* lse, void* workspace, size_t workspace_bytes, int64_t B,
+              int64_t H, int64_t KVH, int64_t T, int64_t D, int dtype, float scale, const int64_t* qo_strides,
+              void* stream) {
+    Workspace w;
+    Lay lq, lk;
+    if (int e = bwd_prologue(workspace, workspace_bytes, B, H, KVH, T, D, dtype, qo_strides, nullptr, &w, &lq, &lk))
+        return e > 0 ? 0 : e;
+    if (!o || !dO || !lse) return fail(-1, "null pointer argument");
+    if (!aligned16(o) || !aligned16(dO)) return fail(-1, "inputs must be 16-byte aligned");
+    if (!(scale > 0.f)) return fail(-1, "scale must be positive");
+    return NNFA_DISPATCH(pre_impl, D, dtype, o, dO, lse, w, B, H, KVH, T, scale, lq, (hipStream_t)stream);
+}
+
+int dkdv_entry(const void* q, const void* k, const void* v, const void* dO, const void* workspace,
+               size_t workspace_bytes, void* dk, void* dv, int64_t B, int64_t H, int64_t KVH, int64_t T, int64_t D,
+               int dtype, float scale, const int64_t* qo_strides, const int64_t* kv_strides, void* stream) {
+    Workspace w;
+    Lay lq, lk;
+    if (int e = bwd_prologue(workspace, workspace_bytes, B, H, KVH, T, D, dtype, qo_strides, kv_strides, &w, &lq, &lk))
+        return e > 0 ? 0 : e;
+    if (!q || !k || !v || !dO || !dk || !dv) return fail(-1, "null pointer argument");
+    if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(dO) || !aligned16(dk) || !aligned16(dv))
+        return fail(-1, "inputs must be 16-byte aligned");
+    return NNFA_DISPATCH(dkdv_impl, D, dtype, q, k, v, dO, w, dk, dv, B, H, KVH, T, scale, lq, lk, (hipStream_t)stream);
+}
+
+int dq_entry(const void* q, const void* k, const void* v, const void* dO, const void* workspace, size_t workspace_bytes,
+             void* dq, int64_t B, int64_t H, int64_t KVH, int64_t T, int64_t D, int dtype, float scale,
+             const int64_t* qo_strides, const int64_t* kv_strides, void* stream) {
+    Workspace w;
+    Lay lq, lk;
+    if (int e = bwd_prologue(workspace, workspace_bytes, B, H, KVH, T, D, dtype, qo_strides, kv_strides, &w, &lq, &lk))
+        return e > 0 ? 0 : e;
+    if (!q || !k || !v || !dO || !dq) return fail(-1, "null pointer argument");
+    if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(dO) || !aligned16(dq))
+        return fail(-1, "inputs must be 16-byte aligned");
+    return NNFA_DISPATCH(dq_impl, D, dtype, q, k, v, dO, w, dq, B, H, KVH, T, scale, lq, lk, (hipStream_t)stream);
+}
+
+int bwd_entry(const void* dO, const void* q, const void* k, const void* v, const void* o, const float* lse, void* dq,
+              void* dk, void* dv, void* workspace, size_t workspace_bytes, int64_t B, int64_t H, int64_t KVH,
+              int64_t T, int64_t D, int dtype, float scale, const int64_t* qo_strides, const int64_t* kv_strides,
+              void* stream) {
+    // Every argument of the three stages is checked before the first launch.
+    Workspace w;
+    Lay lq, lk;
+    if (int e = bwd_prologue(workspace, workspace_bytes, B, H, KVH, T, D, dtype, qo_strides, kv_strides, &w, &lq, &lk))
+        return e > 0 ? 0 : e;
+    if (!dO || !q || !k || !v || !o || !lse || !dq || !dk || !dv) return fail(-1, "null pointer argument");
+    if (!aligned16(dO) || !aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o) || !aligned16(dq) ||
+        !aligned16(dk) || !aligned16(dv))
+        return fail(-1, "inputs must be 16-byte aligned");
+    if (!(scale > 0.f)) return fail(-1, "scale must be positive");
+    if (int e = pre_entry(o, dO, lse, workspace, workspace_bytes, B, H, KVH, T, D, dtype, scale, qo_strides, stream))
+        return e;
+    if (int e = dkdv_entry(q, k, v, dO, workspace, workspace_bytes, dk, dv, B, H, KVH, T, D, dtype, scale, qo_strides,
+                           kv_strides, stream))
+        return e;
+    return dq_entry(q, k, v, dO, workspace, workspace_bytes, dq, B, H, KVH, T, D, dtype, scale, qo_strides, kv_strides,
+                    stream);
+}
+
+}  // namespace
+
+NNFA_API int nn_fa_fwd(const void* q, const void* k, const void* v, void* o, float* lse, int64_t B, int64_t H,
+                       int64_t KVH, int64_t T, int64_t D, int dtype, float scale, void* stream) {
+    return fwd_entry(q, k, v, o, lse, B, H, KVH, T, D, dtype, scale, nullptr, nullptr, stream);
+}
+
+NNFA_API int nn_fa_fwd_strided(const void* q, const void* k, const void* v, void* o, float* lse, int64_t B, int64_t H,
+                               int64_t KVH, int64_t T, int64_t D, const int64_t* qo_strides, const int64_t* kv_strides,
+                               int dtype, float scale, void* stream) {
+    if (!qo_strides || !kv_strides) return fail(-1, "null strides");
+    return fwd_entry(q, k, v, o, lse, B, H, KVH, T, D, dtype, scale, qo_strides, kv_strides, stream);
 }
 
 NNFA_API int nn_fa_bwd_pre(const void* o, const void* dO, const float* lse, void* workspace, size_t workspace_bytes,
                            int64_t B, int64_t H, int64_t KVH, int64_t T, int64_t D, int dtype, float scale,
                            void* stream) {
-    g_last_error.clear();
-    if (int e = check_dims(B, H, KVH, T, D, dtype)) return e;
-    if (B == 0 || T == 0) return 0;
-    if (int e = check_ws(workspace, workspace_bytes, B, H, T)) return e;
-    if (!o || !dO || !lse) return fail(-1, "null pointer argument");
-    if (!aligned16(o) || !aligned16(dO)) return fail(-1, "inputs must be 16-byte aligned");
-    const Workspace w = carve(workspace, B, H, T);
-    if (!(scale > 0.f)) return fail(-1, "scale must be positive");
-    return NNFA_DISPATCH(pre_impl, D, dtype, o, dO, lse, w, B, H, KVH, T, scale, (hipStream_t)stream);
+    return pre_entry(o, dO, lse, workspace, workspace_bytes, B, H, KVH, T, D, dtype, scale, nullptr, stream);
 }
 
 NNFA_API int nn_fa_bwd_dkdv(const void* q, const void* k, const void* v, const void* dO, const void* workspace,
                             size_t workspace_bytes, void* dk, void* dv, int64_t B, int64_t H, int64_t KVH, int64_t T,
                             int64_t D, int dtype, float scale, void* stream) {
-    g_last_error.clear();
-    if (int e = check_dims(B, H, KVH, T, D, dtype)) return e;
-    if (B == 0 || T == 0) return 0;
-    if (int e = check_ws((void*)workspace, workspace_bytes, B, H, T)) return e;
-    if (!q || !k || !v || !dO || !dk || !dv) return fail(-1, "null pointer argument");
-    if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(dO) || !aligned16(dk) || !aligned16(dv))
-        return fail(-1, "inputs must be 16-byte aligned");
-    const Workspace w = carve((void*)workspace, B, H, T);
-    return NNFA_DISPATCH(dkdv_impl, D, dtype, q, k, v, dO, w, dk, dv, B, H, KVH, T, scale, (hipStream_t)stream);
+    return dkdv_entry(q, k, v, dO, workspace, workspace_bytes, dk, dv, B, H, KVH, T, D, dtype, scale, nullptr, nullptr,
+                      stream);
 }
 
 NNFA_API int nn_fa_bwd_dq(const void* q, const void* k, const void* v, const void* dO, const void* workspace,
                           size_t workspace_bytes, void* dq, int64_t B, int64_t H, int64_t KVH, int64_t T, int64_t D,
                           int dtype, float scale, void* stream) {
-    g_last_error.clear();
-    if (int e = check_dims(B, H, KVH, T, D, dtype)) return e;
-    if (B == 0 || T == 0) return 0;
-    if (int e = check_ws((void*)workspace, workspace_bytes, B, H, T)) return e;
-    if (!q || !k || !v || !dO || !dq) return fail(-1, "null pointer argument");
-    if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(dO) || !aligned16(dq))
-        return fail(-1, "inputs must be 16-byte aligned");
-    const Workspace w = carve((void*)workspace, B, H, T);
-    return NNFA_DISPATCH(dq_impl, D, dtype, q, k, v, dO, w, dq, B, H, KVH, T, scale, (hipStream_t)stream);
+    return dq_entry(q, k, v, dO, workspace, workspace_bytes, dq, B, H, KVH, T, D, dtype, scale, nullptr, nullptr,
+                    stream);
 }
 
 NNFA_API int nn_fa_bwd(const void* dO, const void* q, const void* k, const void* v, const void* o, const float* lse,
                        void* dq, void* dk, void* dv, void* workspace, size_t workspace_bytes, int64_t B, int64_t H,
                        int64_t KVH, int64_t T, int64_t D, int dtype, float scale, void* stream) {
-    if (int e = nn_fa_bwd_pre(o, dO, lse, workspace, workspace_bytes, B, H, KVH, T, D, dtype, scale, stream)) return e;
-    if (int e = nn_fa_bwd_dkdv(q, k, v, dO, workspace, workspace_bytes, dk, dv, B, H, KVH, T, D, dtype, scale, stream))
-        return e;
-    return nn_fa_bwd_dq(q, k, v, dO, workspace, workspace_bytes, dq, B, H, KVH, T, D, dtype, scale, stream);
+    return bwd_entry(dO, q, k, v, o, lse, dq, dk, dv, workspace, workspace_bytes, B, H, KVH, T, D, dtype, scale,
+                     nullptr, nullptr, stream);
+}
+
+NNFA_API int nn_fa_bwd_strided(const void* dO, const void* q, const void* k, const void* v, const void* o,
+                               const float* lse, void* dq, void* dk, void* dv, void* workspace, size_t workspace_bytes,
+                               int64_t B, int64_t H, int64_t KVH, int64_t T, int64_t D, const int64_t* qo_strides,
+                               const int64_t* kv_strides, int dtype, float scale, void* stream) {
+    if (!qo_strides || !kv_strides) return fail(-1, "null strides");
+    return bwd_entry(dO, q, k, v, o, lse, dq, dk, dv, workspace, workspace_bytes, B, H, KVH, T, D, dtype, scale,
+                     qo_strides, kv_strides, stream);
 }

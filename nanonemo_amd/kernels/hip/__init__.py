@@ -25,14 +25,24 @@ _vp = ctypes.c_void_p
 _int = ctypes.c_int
 _f32 = ctypes.c_float
 _sz = ctypes.c_size_t
+_i64p = ctypes.POINTER(ctypes.c_int64)
 
 # name -> (restype, argtypes); must match include/nanonemo_fa.h
 SIGNATURES: dict[str, tuple] = {
     "nn_fa_fwd": (_int, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _int, _f32, _vp]),
+    "nn_fa_fwd_strided": (
+        _int,
+        [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64p, _i64p, _int, _f32, _vp],
+    ),
     "nn_fa_bwd_workspace_size": (_sz, [_i64, _i64, _i64, _i64, _i64]),
     "nn_fa_bwd": (
         _int,
         [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _i64, _i64, _i64, _i64, _i64, _int, _f32, _vp],
+    ),
+    "nn_fa_bwd_strided": (
+        _int,
+        [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _i64, _i64, _i64, _i64, _i64, _i64p, _i64p, _int, _f32,
+         _vp],
     ),
     "nn_fa_bwd_pre": (_int, [_vp, _vp, _vp, _vp, _sz, _i64, _i64, _i64, _i64, _i64, _int, _f32, _vp]),
     "nn_fa_bwd_dkdv": (_int, [_vp, _vp, _vp, _vp, _vp, _sz, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _int, _f32, _vp]),
@@ -41,7 +51,7 @@ SIGNATURES: dict[str, tuple] = {
     "nn_fa_abi_version": (_int, []),
 }
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 
 @cache
@@ -60,6 +70,11 @@ def lib() -> ctypes.CDLL:
     if handle.nn_fa_abi_version() != ABI_VERSION:
         raise RuntimeError(f"{LIB_PATH} has ABI {handle.nn_fa_abi_version()}, expected {ABI_VERSION}; rebuild it")
     return handle
+
+
+def strides3(b: int, h: int, t: int) -> ctypes.Array:
+    """An int64[3] {batch, head, row} element-stride array for the *_strided entry points."""
+    return (ctypes.c_int64 * 3)(b, h, t)
 
 
 def check(rc: int) -> None:

@@ -15,18 +15,23 @@ synchronises or copies to the host, so both ops can be captured into a HIP graph
 
 from __future__ import annotations
 
+import ctypes
 import math
 
 import torch
 from torch import Tensor
 
-from nanonemo_amd.kernels.hip import DTYPE_BF16, DTYPE_F16, check, lib
+from nanonemo_amd.kernels.hip import DTYPE_BF16, DTYPE_F16, check, lib, strides3
 
 _DTYPES = {torch.float16: DTYPE_F16, torch.bfloat16: DTYPE_BF16}
 
 
-def _check_inputs(q: Tensor, k: Tensor, v: Tensor) -> None:
-    """The reference's check_inputs (flash_attn.cu:342-356) with the dtype set widened to {fp16, bf16}."""
+def _check_inputs(q: Tensor, k: Tensor, v: Tensor, seq_dim: int = 2) -> None:
+    """The reference's check_inputs (flash_attn.cu:342-356) with the dtype set widened to {fp16, bf16}.
+
+    ``seq_dim`` is 2 for the reference's (B, heads, T, hd) tensors and 1 for the (B, T, heads, hd)
+    tensors of the layout-fused ops; the head dimension is the other one of dims 1 and 2."""
+    head_dim_idx = 3 - seq_dim
     if not (q.is_cuda and k.is_cuda and v.is_cuda):
         raise RuntimeError("inputs must be CUDA tensors")
     if q.dtype not in _DTYPES or k.dtype != q.dtype or v.dtype != q.dtype:
@@ -35,13 +40,13 @@ def _check_inputs(q: Tensor, k: Tensor, v: Tensor) -> None:
         raise RuntimeError("expected (B, H, T, hd) / (B, KVH, T, hd)")
     if not (q.is_contiguous() and k.is_contiguous() and v.is_contiguous()):
         raise RuntimeError("inputs must be contiguous")
-    if q.size(0) != k.size(0) or q.size(2) != k.size(2) or k.shape != v.shape:
+    if q.size(0) != k.size(0) or q.size(seq_dim) != k.size(seq_dim) or k.shape != v.shape:
         raise RuntimeError("K and V must share shape; Q must share batch and length")
     if q.size(3) != k.size(3):
         raise RuntimeError("Q and K must share head_dim")
     if q.size(3) not in (32, 64):
         raise RuntimeError("head_dim must be 32 or 64")
-    if k.size(1) == 0 or q.size(1) % k.size(1) != 0:
+    if k.size(head_dim_idx) == 0 or q.size(head_dim_idx) % k.size(head_dim_idx) != 0:
         raise RuntimeError("query heads must group evenly over KV heads")
     if q.device != k.device or q.device != v.device:
         raise RuntimeError("inputs must be on the same device")
@@ -135,4 +140,97 @@ _flash_attn.register_autograd(_backward, setup_context=_setup_context)
 def flash_attn(q: Tensor, k: Tensor, v: Tensor) -> Tensor:
     """Causal GQA attention. q: (B, H, T, hd), k/v: (B, KVH, T, hd), fp16 or bf16, H % KVH == 0, hd in {32, 64}."""
     o, _ = _flash_attn(q, k, v)
+    return o
+
+
+# ---- layout-fused ops: (B, T, heads, hd) in and out -------------------------------------------
+# The reference model projects x to (B, T, heads * hd), views it as (B, T, heads, hd), transposes to
+# (B, heads, T, hd) for the op (which then copies each input to contiguous memory,
+# /root/reference/nanonemo/kernels/cuda/flash_attn.py:20,33) and transposes + reshapes o back for
+# the output projection (/root/reference/nanonemo/model/layers.py:97-104,116), one more copy per
+# direction. These ops take and return the projection layout itself through the library's strided
+# entry points: q (B, T, H, hd), k / v (B, T, KVH, hd), o / dq (B, T, H, hd), dk / dv (B, T, KVH, hd),
+# all contiguous in that layout (so o.view(B, T, H * hd) feeds the output projection directly);
+# lse stays (B, H, T). Not in the reference: an addition that the same model code can select.
+
+
+def _bthd_strides(t: Tensor) -> ctypes.Array:
+    B, T, Hh, D = t.shape
+    return strides3(T * Hh * D, D, Hh * D)
+
+
+@torch.library.custom_op("nanonemo::flash_attn_bthd", mutates_args=())
+def _flash_attn_bthd(q: Tensor, k: Tensor, v: Tensor) -> tuple[Tensor, Tensor]:
+    q, k, v = _contig(q), _contig(k), _contig(v)
+    _check_inputs(q, k, v, seq_dim=1)
+    B, T, H, D = q.shape
+    KVH = k.size(2)
+    o = torch.empty_like(q, memory_format=torch.contiguous_format)
+    lse = torch.empty((B, H, T), dtype=torch.float32, device=q.device)
+    if B == 0 or T == 0 or H == 0:
+        return o, lse
+    with torch.cuda.device(q.device):
+        rc = lib().nn_fa_fwd_strided(
+            q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(),
+            B, H, KVH, T, D, _bthd_strides(q), _bthd_strides(k), _DTYPES[q.dtype], 1.0 / math.sqrt(D), _stream(q),
+        )
+    check(rc)
+    return o, lse
+
+
+@_flash_attn_bthd.register_fake
+def _(q, k, v):
+    B, T, H, _ = q.shape
+    return (
+        torch.empty(q.shape, dtype=q.dtype, device=q.device),
+        torch.empty((B, H, T), dtype=torch.float32, device=q.device),
+    )
+
+
+@torch.library.custom_op("nanonemo::flash_attn_bthd_bwd", mutates_args=())
+def _flash_attn_bthd_bwd(
+    d_o: Tensor, q: Tensor, k: Tensor, v: Tensor, o: Tensor, lse: Tensor
+) -> tuple[Tensor, Tensor, Tensor]:
+    d_o, q, k, v, o, lse = (_contig(t) for t in (d_o, q, k, v, o, lse))
+    _check_inputs(q, k, v, seq_dim=1)
+    if d_o.shape != q.shape or d_o.dtype != q.dtype or o.shape != q.shape or o.dtype != q.dtype:
+        raise RuntimeError("d_o must be a contiguous float16/bfloat16 tensor shaped like q")
+    B, T, H, D = q.shape
+    KVH = k.size(2)
+    if lse.shape != (B, H, T) or lse.dtype != torch.float32:
+        raise RuntimeError("lse must be a float32 tensor of shape (B, H, T)")
+    dq = torch.empty_like(q, memory_format=torch.contiguous_format)
+    dk = torch.empty_like(k, memory_format=torch.contiguous_format)
+    dv = torch.empty_like(v, memory_format=torch.contiguous_format)
+    if B == 0 or T == 0 or H == 0:
+        return dq, dk, dv
+    L = lib()
+    ws_bytes = L.nn_fa_bwd_workspace_size(B, H, KVH, T, D)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device)
+    with torch.cuda.device(q.device):
+        rc = L.nn_fa_bwd_strided(
+            d_o.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(),
+            dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), ws.data_ptr(), ws_bytes,
+            B, H, KVH, T, D, _bthd_strides(q), _bthd_strides(k), _DTYPES[q.dtype], 1.0 / math.sqrt(D), _stream(q),
+        )
+    check(rc)
+    return dq, dk, dv
+
+
+@_flash_attn_bthd_bwd.register_fake
+def _(d_o, q, k, v, o, lse):
+    return tuple(torch.empty(t.shape, dtype=t.dtype, device=t.device) for t in (q, k, v))
+
+
+def _backward_bthd(ctx, d_o, _d_lse):
+    q, k, v, o, lse = ctx.saved_tensors
+    return _flash_attn_bthd_bwd(d_o, q, k, v, o, lse)
+
+
+_flash_attn_bthd.register_autograd(_backward_bthd, setup_context=_setup_context)
+
+
+def flash_attn_bthd(q: Tensor, k: Tensor, v: Tensor) -> Tensor:
+    """Causal GQA attention in the projection layout: q (B, T, H, hd), k/v (B, T, KVH, hd) -> o (B, T, H, hd)."""
+    o, _ = _flash_attn_bthd(q, k, v)
     return o

@@ -80,6 +80,29 @@ def test_c_abi_rejects_misaligned_and_small_workspace():
     assert rc != 0 and "null workspace" in L.nn_fa_last_error().decode()
 
 
+@pytest.mark.parametrize(
+    "qs, ks, msg",
+    [
+        ((4096, 1024, 60), (4096, 1024, 64), "q/o strides must be positive multiples of 8"),
+        ((4096, 1024, 64), (4096, 0, 64), "k/v strides must be positive multiples of 8"),
+        ((4096, 1024, 32), (4096, 1024, 64), "q/o row stride is smaller than head_dim"),
+        ((4096, 1024, 1 << 27), (4096, 1024, 64), "q/o strides too large"),
+    ],
+)
+def test_strided_c_abi_rejects_bad_strides_before_any_launch(qs, ks, msg):
+    from nanonemo_amd.kernels.hip import strides3
+
+    L = lib()
+    B, H, KVH, T, D = 1, 4, 2, 16, 64
+    rc = L.nn_fa_fwd_strided(16, 16, 16, 16, 16, B, H, KVH, T, D, strides3(*qs), strides3(*ks), 1, 0.125, None)
+    assert rc != 0 and msg in L.nn_fa_last_error().decode()
+    rc = L.nn_fa_bwd_strided(16, 16, 16, 16, 16, 16, 16, 16, 16, 256, 1 << 30, B, H, KVH, T, D,
+                             strides3(*qs), strides3(*ks), 1, 0.125, None)
+    assert rc != 0 and msg in L.nn_fa_last_error().decode()
+    rc = L.nn_fa_fwd_strided(16, 16, 16, 16, 16, B, H, KVH, T, D, None, strides3(*ks), 1, 0.125, None)
+    assert rc != 0 and "null strides" in L.nn_fa_last_error().decode()
+
+
 def test_c_abi_empty_problem_is_a_no_op():
     # T == 0 and B == 0 return success without touching device memory (flash_attn.cu:367).
     L = lib()
@@ -106,6 +129,29 @@ def test_ops_registered_with_reference_schemas():
         "nanonemo::flash_attn_bwd(Tensor d_o, Tensor q, Tensor k, Tensor v, Tensor o, Tensor lse)"
         " -> (Tensor, Tensor, Tensor)"
     )
+
+
+def test_layout_fused_ops_registered():
+    _ops()
+    fwd = torch.ops.nanonemo.flash_attn_bthd.default._schema
+    bwd = torch.ops.nanonemo.flash_attn_bthd_bwd.default._schema
+    assert str(fwd) == "nanonemo::flash_attn_bthd(Tensor q, Tensor k, Tensor v) -> (Tensor, Tensor)"
+    assert str(bwd) == (
+        "nanonemo::flash_attn_bthd_bwd(Tensor d_o, Tensor q, Tensor k, Tensor v, Tensor o, Tensor lse)"
+        " -> (Tensor, Tensor, Tensor)"
+    )
+
+
+def test_layout_fused_fakes_keep_the_projection_layout():
+    fa = _ops()
+    B, T, H, KVH, D = 2, 64, 12, 4, 64
+    q = torch.empty(B, T, H, D, dtype=torch.bfloat16, device="meta")
+    k = torch.empty(B, T, KVH, D, dtype=torch.bfloat16, device="meta")
+    o, lse = torch.ops.nanonemo.flash_attn_bthd(q, k, k)
+    assert o.shape == (B, T, H, D) and o.is_contiguous() and lse.shape == (B, H, T) and lse.dtype == torch.float32
+    dq, dk, dv = torch.ops.nanonemo.flash_attn_bthd_bwd(o, q, k, k, o, lse)
+    assert dq.shape == q.shape and dk.shape == k.shape and dv.shape == k.shape
+    assert fa.flash_attn_bthd(q, k, k).view(B, T, H * D).shape == (B, T, H * D)
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
