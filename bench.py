@@ -20,7 +20,10 @@ The JSON line also carries:
                 the dense BF16/FP16 MFMA peak of 2.5 PFLOP/s;
   cpu_baseline  the reference's plain-PyTorch attention (repeat_interleave + SDPA math, forward +
                 autograd) in fp32 on the host cores, on a bounded sample of the same workload;
-  kernels       per-kernel mean times and the preprocessing pass's HBM rate.
+  kernels       per-kernel mean times and the preprocessing pass's HBM rate;
+  layout_fusion the same fwd+bwd from (B, T, heads, hd) projections: through transposed views and the
+                dense ops (the reference model's flow, with its copies) vs the layout-fused
+                nanonemo::flash_attn_bthd ops.
 """
 
 from __future__ import annotations
@@ -59,6 +62,7 @@ def parse():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="budget of the CPU baseline sample")
     p.add_argument("--profile-only", action="store_true", help="only the timed steps (for rocprofv3)")
+    p.add_argument("--prewarm", type=float, default=1.0, help="seconds of untimed steps before the warmup")
     return p.parse_args()
 
 
@@ -171,10 +175,12 @@ def main():
         torch.cuda.synchronize()
         return (time.perf_counter() - t0) * 1e3 / n
 
-    # Untimed: about 0.3 s of steps first, so that the device clocks have settled, then the W warmup steps.
-    t_end = time.perf_counter() + 0.3
+    # Untimed: about 1 s of back-to-back steps first (the device clocks take that long to settle
+    # under this load; step times measured earlier are up to 10 % longer), then the W warmup steps.
+    t_end = time.perf_counter() + args.prewarm
     while time.perf_counter() < t_end:
-        step_abi()
+        for _ in range(20):
+            step_abi()
         torch.cuda.synchronize()
     for _ in range(args.warmup):
         step_abi()
@@ -191,6 +197,30 @@ def main():
         torch.cuda.synchronize()
         print(json.dumps({"ms_per_step": ms, "op_ms_per_step": op_ms, "copy_calib_bytes": COPY_CALIB_BYTES}), flush=True)
         return
+
+    # ---- layout fusion: the same fwd+bwd starting from the projection layout (B, T, heads, hd) ----
+    # "views": the reference model's flow (layers.py:97-104,116) -- transposed views into the dense ops,
+    # which copy them to contiguous memory, then o transposed + reshaped for the output projection and
+    # the gradients transposed back to the projection layout. "fused": nanonemo::flash_attn_bthd, which
+    # reads and writes that layout directly.
+    qp, kp, vp, dop = (t.transpose(1, 2).contiguous() for t in (q, k, v, do))
+
+    def step_views():
+        o2, lse2 = fa._flash_attn(qp.transpose(1, 2), kp.transpose(1, 2), vp.transpose(1, 2))
+        y = o2.transpose(1, 2).reshape(B, T, H * D)
+        g = fa._flash_attn_bwd(dop.transpose(1, 2), qp.transpose(1, 2), kp.transpose(1, 2), vp.transpose(1, 2), o2, lse2)
+        return y, [t.transpose(1, 2).contiguous() for t in g]
+
+    def step_fused():
+        o2, lse2 = fa._flash_attn_bthd(qp, kp, vp)
+        y = o2.view(B, T, H * D)
+        return y, fa._flash_attn_bthd_bwd(dop, qp, kp, vp, o2, lse2)
+
+    for _ in range(3):
+        step_views()
+        step_fused()
+    views_ms = timed(step_views, args.steps)
+    fused_ms = timed(step_fused, args.steps)
 
     # ---- each kernel alone, HIP events on the launch stream ----
     launches = {
@@ -262,6 +292,12 @@ def main():
         },
         "pct_of_bf16_peak": round(100 * value / PEAK_TFLOPS, 2),
         "op_ms_per_step": round(op_ms, 5),
+        "layout_fusion": {
+            "from": "projection layout (B, T, heads, hd)",
+            "views_ms_per_step": round(views_ms, 5),
+            "fused_ms_per_step": round(fused_ms, 5),
+            "speedup": round(views_ms / fused_ms, 3),
+        },
         "roofline": {
             "kernel": kernel_names[dominant],
             "bound": "mfma",
