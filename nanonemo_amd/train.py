@@ -1,0 +1,110 @@
+"""bf16 training step of the 114 M model on the attention ops, and the config-5 comparison run.
+
+``train_step`` follows the reference's (/root/reference/nanonemo/train/trainer.py:150-194) for one
+process: micro-batches under bf16 autocast, loss / accum backpropagated, gradient clipping on the
+pre-clip global norm, optimizer step, zero_grad. The reference's distributed hooks and fp16 loss
+scaler are not needed here (bf16, one GPU).
+
+    python -m nanonemo_amd.train [--steps 50] [--batch 8] [--seq 1024] [--attn torch hip hip_bthd]
+
+runs BASELINE config 5: the 114 M model, random init (seed 0), uniform synthetic token ids in
+[0, vocab), the same initial weights and batches for every attention kernel, and prints one JSON line
+with tokens/s per kernel and the largest per-step loss difference from the "torch" (SDPA) path.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import time
+
+import torch
+
+from nanonemo_amd.model import ModelConfig, NanoNemo
+
+
+def train_step(model, opt, batches, grad_clip: float = 1.0, amp_dtype=torch.bfloat16):
+    """One optimizer step over the micro-batches ``batches`` [(x, y), ...]; returns (loss, grad_norm)
+    as device tensors (no host synchronisation)."""
+    accum = len(batches)
+    loss_sum = None
+    for x, y in batches:
+        with torch.autocast(x.device.type, dtype=amp_dtype, enabled=amp_dtype is not None):
+            _, loss = model(x, y)
+        loss = loss / accum
+        loss.backward()
+        loss = loss.detach()
+        loss_sum = loss if loss_sum is None else loss_sum + loss
+    grad_norm = torch.nn.utils.clip_grad_norm_(model.parameters(), grad_clip)
+    opt.step()
+    opt.zero_grad(set_to_none=True)
+    return loss_sum, grad_norm
+
+
+def synthetic_batches(steps: int, batch: int, seq: int, vocab: int, device, seed: int = 0):
+    """Uniform token ids; targets are the inputs shifted by one (the last target wraps)."""
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    out = []
+    for _ in range(steps):
+        idx = torch.randint(0, vocab, (batch, seq + 1), generator=g)
+        out.append((idx[:, :-1].to(device), idx[:, 1:].to(device)))
+    return out
+
+
+def make_optimizer(model, lr: float = 6e-4):
+    decay = [p for p in model.parameters() if p.dim() >= 2]
+    no_decay = [p for p in model.parameters() if p.dim() < 2]
+    return torch.optim.AdamW(
+        [{"params": decay, "weight_decay": 0.1}, {"params": no_decay, "weight_decay": 0.0}],
+        lr=lr, betas=(0.9, 0.95), fused=True,
+    )
+
+
+def run(attn: str, steps: int, batch: int, seq: int, cfg_kwargs: dict, device: str = "cuda", warmup: int = 3):
+    """Train ``steps`` steps from the seed-0 init on the seed-0 synthetic stream; returns the per-step
+    losses and the tokens/s over the steps after ``warmup``."""
+    torch.manual_seed(0)
+    model = NanoNemo(ModelConfig(**cfg_kwargs, attn_kernel=attn)).to(device)
+    opt = make_optimizer(model)
+    data = synthetic_batches(steps, batch, seq, model.cfg.vocab_size, device)
+    losses = []
+    t0 = None
+    for i, (x, y) in enumerate(data):
+        if i == warmup:
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+        loss, _ = train_step(model, opt, [(x, y)])
+        losses.append(loss)
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0 if t0 is not None else float("nan")
+    tokens = (steps - warmup) * batch * seq
+    return [float(v) for v in torch.stack(losses).cpu()], tokens / dt, model.flops_per_token(seq)
+
+
+def main():
+    p = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    p.add_argument("--steps", type=int, default=50)
+    p.add_argument("--batch", type=int, default=8)
+    p.add_argument("--seq", type=int, default=1024)
+    p.add_argument("--attn", nargs="+", default=["torch", "hip", "hip_bthd"])
+    p.add_argument("--small", action="store_true", help="a 2-layer model (quick check)")
+    a = p.parse_args()
+    cfg_kwargs = dict(n_layers=2, d_model=256, n_heads=4, n_kv_heads=2, d_ff=512, vocab_size=512, max_seq_len=a.seq) \
+        if a.small else dict(max_seq_len=a.seq)
+    res = {}
+    for attn in a.attn:
+        losses, tps, fpt = run(attn, a.steps, a.batch, a.seq, cfg_kwargs)
+        res[attn] = {"tokens_per_s": round(tps, 1), "model_tflops": round(tps * fpt / 1e12, 2), "loss_first": losses[0],
+                     "loss_last": losses[-1], "losses": [round(v, 5) for v in losses]}
+        print(f"[train] attn={attn}: {tps:,.0f} tokens/s, loss {losses[0]:.4f} -> {losses[-1]:.4f}", flush=True)
+    if "torch" in res:
+        for attn in res:
+            if attn != "torch":
+                d = [abs(x - y) for x, y in zip(res[attn]["losses"], res["torch"]["losses"])]
+                res[attn]["max_abs_loss_diff_vs_torch"] = round(max(d), 5)
+    print(json.dumps({"workload": f"114M NanoNemo bf16 autocast, B={a.batch} T={a.seq}, {a.steps} AdamW steps, "
+                      "seed 0, uniform synthetic tokens", "results": res}), flush=True)
+
+
+if __name__ == "__main__":
+    main()

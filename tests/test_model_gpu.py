@@ -1,0 +1,89 @@
+"""The model with this build's attention against the same model on the plain-PyTorch attention, on
+identical weights and inputs (the pattern of /root/reference/tests/kernels/test_model_kernels.py:54-78),
+plus the layout-fused path's exact agreement with the drop-in path, torch.compile, and a short
+training run (BASELINE config 5 in miniature)."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from nanonemo_amd.model import ModelConfig, NanoNemo
+from nanonemo_amd.train import make_optimizer, synthetic_batches, train_step
+
+pytestmark = pytest.mark.gpu
+
+SMALL = dict(n_layers=2, d_model=256, n_heads=4, n_kv_heads=2, d_ff=512, vocab_size=512, max_seq_len=128)
+
+
+def _pair(attn: str):
+    torch.manual_seed(0)
+    ref = NanoNemo(ModelConfig(**SMALL)).cuda()
+    fast = NanoNemo(ModelConfig(**SMALL, attn_kernel=attn)).cuda()
+    fast.load_state_dict(ref.state_dict())
+    idx = torch.randint(0, SMALL["vocab_size"], (2, 128), device="cuda")
+    return ref, fast, idx, torch.roll(idx, -1, dims=1)
+
+
+def _grads(model):
+    return {n: p.grad for n, p in model.named_parameters()}
+
+
+@pytest.mark.parametrize("attn", ["hip", "hip_bthd"])
+def test_bf16_autocast_loss_and_grads_match_torch_attention(attn):
+    print(f"\n[case] model {attn} vs torch attention, bf16 autocast", flush=True)
+    ref, fast, idx, tgt = _pair(attn)
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        _, ref_loss = ref(idx, tgt)
+        _, loss = fast(idx, tgt)
+    # bf16 rounds 8x coarser than the reference's fp16 test (loss 1e-3, grads 5e-2 * max)
+    torch.testing.assert_close(loss, ref_loss, rtol=5e-3, atol=5e-3)
+    ref_loss.backward()
+    loss.backward()
+    for name, g in _grads(fast).items():
+        r = _grads(ref)[name]
+        torch.testing.assert_close(g, r, rtol=5e-2, atol=5e-2 * r.abs().max().item(), msg=name)
+
+
+def test_layout_fused_model_is_bit_identical_to_the_drop_in_model():
+    _, a, idx, tgt = _pair("hip")
+    torch.manual_seed(0)
+    b = NanoNemo(ModelConfig(**SMALL, attn_kernel="hip_bthd")).cuda()
+    b.load_state_dict(a.state_dict())
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        la = a(idx, tgt)[1]
+        lb = b(idx, tgt)[1]
+    la.backward()
+    lb.backward()
+    assert torch.equal(la, lb)
+    for (n, ga), gb in zip(_grads(a).items(), _grads(b).values()):
+        assert torch.equal(ga, gb), n
+
+
+def test_compiled_model_has_no_graph_breaks():
+    _, fast, idx, tgt = _pair("hip_bthd")
+    torch._dynamo.reset()
+    compiled = torch.compile(fast, fullgraph=True)
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        _, loss = compiled(idx, tgt)
+        _, eager_loss = fast(idx, tgt)
+    loss.backward()
+    torch.testing.assert_close(loss, eager_loss, rtol=1e-3, atol=1e-3)
+
+
+def test_short_training_run_tracks_torch_attention():
+    curves = {}
+    for attn in ("torch", "hip_bthd"):
+        torch.manual_seed(0)
+        model = NanoNemo(ModelConfig(**SMALL, attn_kernel=attn)).cuda()
+        opt = make_optimizer(model, lr=2e-3)
+        # one fixed batch, so that the loss has something to learn (uniform random streams do not)
+        batch = synthetic_batches(1, 4, 128, SMALL["vocab_size"], "cuda")[0]
+        curves[attn] = torch.stack([train_step(model, opt, [batch])[0] for _ in range(10)]).cpu()
+    print(f"\n[train] torch {curves['torch'].tolist()}\n[train] hip   {curves['hip_bthd'].tolist()}", flush=True)
+    assert torch.isfinite(curves["hip_bthd"]).all()
+    # Two bf16 runs drift apart step by step (different rounding, then different updates), as any two
+    # kernels do: the first steps agree closely, the whole curve within a few percent.
+    torch.testing.assert_close(curves["hip_bthd"][:5], curves["torch"][:5], rtol=0, atol=2e-2)
+    torch.testing.assert_close(curves["hip_bthd"], curves["torch"], rtol=5e-2, atol=0)
+    assert curves["hip_bthd"][-1] < curves["hip_bthd"][0] - 0.5
