@@ -55,8 +55,9 @@ int nn_fa_fwd_strided(const void* q, const void* k, const void* v, void* o, floa
 size_t nn_fa_bwd_workspace_size(int64_t B, int64_t H, int64_t KVH, int64_t T, int64_t D);
 
 /* Backward: (dq, dk, dv) in the input dtype, contiguous. dk/dv hold the sum over the
- * H / KVH query heads that share each KV head. Runs nn_fa_bwd_pre, nn_fa_bwd_dkdv and
- * nn_fa_bwd_dq in that order on `stream`. Deterministic: no atomics.
+ * H / KVH query heads that share each KV head. Runs nn_fa_bwd_dq (which also performs the
+ * preprocessing pass into the workspace) and then nn_fa_bwd_dkdv on `stream`. Deterministic:
+ * no atomics.
  * Replaces the pybind `bwd(d_o, q, k, v, o, lse) -> (dq, dk, dv)` of
  * /root/reference/nanonemo/kernels/cuda/flash_attn.cu:381-405 (kernel :176-340),
  * bound at /root/reference/nanonemo/kernels/cuda/flash_attn.py:31-35. */
@@ -76,23 +77,27 @@ int nn_fa_bwd_strided(const void* dO, const void* q, const void* k, const void* 
                       const int64_t qo_strides[3], const int64_t kv_strides[3],
                       int dtype, float scale, void* stream);
 
-/* Backward, stage 1: -D = -rowsum(dO * o) and -lse / scale, fp32, into the workspace.
- * Replaces the ATen preprocessing inside flash_bwd, flash_attn.cu:387-391. */
+/* Backward preprocessing alone: -D = -rowsum(dO * o) and -lse / scale, fp32, into the workspace.
+ * Replaces the ATen preprocessing inside flash_bwd, flash_attn.cu:387-391. nn_fa_bwd does not call
+ * it (nn_fa_bwd_dq performs the same pass in its prologue); it prepares the workspace for a caller
+ * that runs nn_fa_bwd_dkdv on its own. */
 int nn_fa_bwd_pre(const void* o, const void* dO, const float* lse, void* workspace, size_t workspace_bytes,
                   int64_t B, int64_t H, int64_t KVH, int64_t T, int64_t D, int dtype, float scale,
                   void* stream);
 
-/* Backward, stage 2: dk and dv (keys outer; recomputes P from the workspace's lse and uses its D).
- * Needs the workspace prepared by nn_fa_bwd_pre. Together with stage 3 it replaces
- * bwd_kernel<HD>, flash_attn.cu:176-340 with its launch at :393-401 and the casts at :404. */
+/* Backward, dk and dv (keys outer; recomputes P from the workspace's -lse/scale and uses its -D).
+ * Needs the workspace prepared by nn_fa_bwd_dq or nn_fa_bwd_pre. Together with nn_fa_bwd_dq it
+ * replaces bwd_kernel<HD>, flash_attn.cu:176-340 with its launch at :393-401 and the casts at :404. */
 int nn_fa_bwd_dkdv(const void* q, const void* k, const void* v, const void* dO,
                    const void* workspace, size_t workspace_bytes, void* dk, void* dv,
                    int64_t B, int64_t H, int64_t KVH, int64_t T, int64_t D,
                    int dtype, float scale, void* stream);
 
-/* Backward, stage 3: dq (queries outer). Needs the workspace prepared by nn_fa_bwd_pre. */
-int nn_fa_bwd_dq(const void* q, const void* k, const void* v, const void* dO,
-                 const void* workspace, size_t workspace_bytes, void* dq,
+/* Backward, dq (queries outer). Also computes -D = -rowsum(dO * o) and -lse / scale for its rows
+ * and writes them into the workspace (the preprocessing pass of flash_attn.cu:387-391, fused), so
+ * nn_fa_bwd_dkdv can run after it. */
+int nn_fa_bwd_dq(const void* q, const void* k, const void* v, const void* o, const void* dO,
+                 const float* lse, void* workspace, size_t workspace_bytes, void* dq,
                  int64_t B, int64_t H, int64_t KVH, int64_t T, int64_t D,
                  int dtype, float scale, void* stream);
 

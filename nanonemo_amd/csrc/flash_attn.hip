@@ -745,11 +745,11 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(
 // ------------------------------------------------------------------------------------------
 template <int HD, int DT>
 __global__ __launch_bounds__(256, 2) void fa_bwd_dq_kernel(const u16* __restrict__ Q, const u16* __restrict__ K,
-                                                           const u16* __restrict__ V, const u16* __restrict__ dO,
-                                                           const float* __restrict__ nLvec,
-                                                           const float* __restrict__ nDvec, u16* __restrict__ dQ, int BH,
-                                                           int H, int KVH, int T, int nqb, float sl2, float scale,
-                                                           Lay lq, Lay lk) {
+                                                           const u16* __restrict__ V, const u16* __restrict__ O,
+                                                           const u16* __restrict__ dO, const float* __restrict__ LSE,
+                                                           float* __restrict__ nLvec, float* __restrict__ nDvec,
+                                                           u16* __restrict__ dQ, int BH, int H, int KVH, int T, int nqb,
+                                                           float sl2, float scale, Lay lq, Lay lk) {
     using E = Elem<DT>;
     constexpr int BM = 128, BN = 64, NW = 4;
     constexpr int NS = HD / 16;
@@ -778,14 +778,26 @@ __global__ __launch_bounds__(256, 2) void fa_bwd_dq_kernel(const u16* __restrict
     const int q0 = qb * BM, qw = q0 + wave * 32, qrow = qw + l32;
     const int qc_ = min(qrow, T - 1);
 
+    // The preprocessing pass, for this block's rows: D = rowsum(dO * O) from the 16-bit O (each half-wave
+    // holds half of a row; one exchange completes it), and -lse/scale. Every query row belongs to exactly
+    // one dQ block, which also writes both into the workspace for the dK/dV kernel that runs next.
     u16x8 qf[NS], gf[NS];
+    float dacc = 0.f;
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
         qf[s] = ld8(Q + qoff + (size_t)qc_ * lq.st + 16 * s + 8 * hh);
         gf[s] = ld8(dO + qoff + (size_t)qc_ * lq.st + 16 * s + 8 * hh);
+        const u16x8 of = ld8(O + qoff + (size_t)qc_ * lq.st + 16 * s + 8 * hh);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) dacc = fmaf(E::to_f32(gf[s][j]), E::to_f32(of[j]), dacc);
     }
-    const float nl2 = nLvec[(size_t)bh * T + qc_] * sl2;  // -lse * log2(e)
-    const float nd = nDvec[(size_t)bh * T + qc_];
+    const float nd = -pair_sum(dacc);
+    const float lse = LSE[(size_t)bh * T + qc_];
+    const float nl2 = -lse * kLog2e;  // (-lse/scale) * sl2
+    if (hh == 0 && qrow < T) {
+        nDvec[(size_t)bh * T + qrow] = nd;
+        nLvec[(size_t)bh * T + qrow] = -lse / scale;
+    }
 
     int koff[NS], kcol[ND][2];
 #pragma unroll
@@ -973,13 +985,14 @@ int dkdv_impl(const void* q, const void* k, const void* v, const void* dO, const
 }
 
 template <int HD, int DT>
-int dq_impl(const void* q, const void* k, const void* v, const void* dO, const Workspace& w, void* dq, int64_t B,
-            int64_t H, int64_t KVH, int64_t T, float scale, Lay lq, Lay lk, hipStream_t st) {
+int dq_impl(const void* q, const void* k, const void* v, const void* o, const void* dO, const float* lse,
+            const Workspace& w, void* dq, int64_t B, int64_t H, int64_t KVH, int64_t T, float scale, Lay lq, Lay lk,
+            hipStream_t st) {
     const int nqb = (int)((T + 127) / 128);
     const int BH = (int)(B * H);
     fa_bwd_dq_kernel<HD, DT><<<dim3(nqb * BH), dim3(256), 0, st>>>(
-        (const u16*)q, (const u16*)k, (const u16*)v, (const u16*)dO, w.nL, w.nD, (u16*)dq, BH, (int)H, (int)KVH,
-        (int)T, nqb, scale * kLog2e, scale, lq, lk);
+        (const u16*)q, (const u16*)k, (const u16*)v, (const u16*)o, (const u16*)dO, lse, w.nL, w.nD, (u16*)dq, BH,
+        (int)H, (int)KVH, (int)T, nqb, scale * kLog2e, scale, lq, lk);
     return launch_status("fa_bwd_dq_kernel");
 }
 
@@ -1020,7 +1033,7 @@ int check_ws(void* workspace, size_t workspace_bytes, int64_t B, int64_t H, int6
 
 NNFA_API const char* nn_fa_last_error(void) { return g_last_error.c_str(); }
 
-NNFA_API int nn_fa_abi_version(void) { return 5; }
+NNFA_API int nn_fa_abi_version(void) { return 6; }
 
 NNFA_API size_t nn_fa_bwd_workspace_size(int64_t B, int64_t H, int64_t KVH, int64_t T, int64_t D) {
     (void)KVH;
@@ -1091,17 +1104,19 @@ int dkdv_entry(const void* q, const void* k, const void* v, const void* dO, cons
     return NNFA_DISPATCH(dkdv_impl, D, dtype, q, k, v, dO, w, dk, dv, B, H, KVH, T, scale, lq, lk, (hipStream_t)stream);
 }
 
-int dq_entry(const void* q, const void* k, const void* v, const void* dO, const void* workspace, size_t workspace_bytes,
-             void* dq, int64_t B, int64_t H, int64_t KVH, int64_t T, int64_t D, int dtype, float scale,
-             const int64_t* qo_strides, const int64_t* kv_strides, void* stream) {
+int dq_entry(const void* q, const void* k, const void* v, const void* o, const void* dO, const float* lse,
+             void* workspace, size_t workspace_bytes, void* dq, int64_t B, int64_t H, int64_t KVH, int64_t T,
+             int64_t D, int dtype, float scale, const int64_t* qo_strides, const int64_t* kv_strides, void* stream) {
     Workspace w;
     Lay lq, lk;
     if (int e = bwd_prologue(workspace, workspace_bytes, B, H, KVH, T, D, dtype, qo_strides, kv_strides, &w, &lq, &lk))
         return e > 0 ? 0 : e;
-    if (!q || !k || !v || !dO || !dq) return fail(-1, "null pointer argument");
-    if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(dO) || !aligned16(dq))
+    if (!q || !k || !v || !o || !dO || !lse || !dq) return fail(-1, "null pointer argument");
+    if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o) || !aligned16(dO) || !aligned16(dq))
         return fail(-1, "inputs must be 16-byte aligned");
-    return NNFA_DISPATCH(dq_impl, D, dtype, q, k, v, dO, w, dq, B, H, KVH, T, scale, lq, lk, (hipStream_t)stream);
+    if (!(scale > 0.f)) return fail(-1, "scale must be positive");
+    return NNFA_DISPATCH(dq_impl, D, dtype, q, k, v, o, dO, lse, w, dq, B, H, KVH, T, scale, lq, lk,
+                         (hipStream_t)stream);
 }
 
 int bwd_entry(const void* dO, const void* q, const void* k, const void* v, const void* o, const float* lse, void* dq,
@@ -1118,13 +1133,13 @@ int bwd_entry(const void* dO, const void* q, const void* k, const void* v, const
         !aligned16(dk) || !aligned16(dv))
         return fail(-1, "inputs must be 16-byte aligned");
     if (!(scale > 0.f)) return fail(-1, "scale must be positive");
-    if (int e = pre_entry(o, dO, lse, workspace, workspace_bytes, B, H, KVH, T, D, dtype, scale, qo_strides, stream))
+    // dQ first: it also computes -D and -lse/scale for its rows into the workspace (the preprocessing
+    // pass, fused), which the dK/dV kernel reads.
+    if (int e = dq_entry(q, k, v, o, dO, lse, workspace, workspace_bytes, dq, B, H, KVH, T, D, dtype, scale, qo_strides,
+                         kv_strides, stream))
         return e;
-    if (int e = dkdv_entry(q, k, v, dO, workspace, workspace_bytes, dk, dv, B, H, KVH, T, D, dtype, scale, qo_strides,
-                           kv_strides, stream))
-        return e;
-    return dq_entry(q, k, v, dO, workspace, workspace_bytes, dq, B, H, KVH, T, D, dtype, scale, qo_strides, kv_strides,
-                    stream);
+    return dkdv_entry(q, k, v, dO, workspace, workspace_bytes, dk, dv, B, H, KVH, T, D, dtype, scale, qo_strides,
+                      kv_strides, stream);
 }
 
 }  // namespace
@@ -1154,11 +1169,11 @@ NNFA_API int nn_fa_bwd_dkdv(const void* q, const void* k, const void* v, const v
                       stream);
 }
 
-NNFA_API int nn_fa_bwd_dq(const void* q, const void* k, const void* v, const void* dO, const void* workspace,
-                          size_t workspace_bytes, void* dq, int64_t B, int64_t H, int64_t KVH, int64_t T, int64_t D,
-                          int dtype, float scale, void* stream) {
-    return dq_entry(q, k, v, dO, workspace, workspace_bytes, dq, B, H, KVH, T, D, dtype, scale, nullptr, nullptr,
-                    stream);
+NNFA_API int nn_fa_bwd_dq(const void* q, const void* k, const void* v, const void* o, const void* dO, const float* lse,
+                          void* workspace, size_t workspace_bytes, void* dq, int64_t B, int64_t H, int64_t KVH,
+                          int64_t T, int64_t D, int dtype, float scale, void* stream) {
+    return dq_entry(q, k, v, o, dO, lse, workspace, workspace_bytes, dq, B, H, KVH, T, D, dtype, scale, nullptr,
+                    nullptr, stream);
 }
 
 NNFA_API int nn_fa_bwd(const void* dO, const void* q, const void* k, const void* v, const void* o, const float* lse,

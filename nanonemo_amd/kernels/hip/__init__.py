@@ -46,12 +46,14 @@ SIGNATURES: dict[str, tuple] = {
     ),
     "nn_fa_bwd_pre": (_int, [_vp, _vp, _vp, _vp, _sz, _i64, _i64, _i64, _i64, _i64, _int, _f32, _vp]),
     "nn_fa_bwd_dkdv": (_int, [_vp, _vp, _vp, _vp, _vp, _sz, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _int, _f32, _vp]),
-    "nn_fa_bwd_dq": (_int, [_vp, _vp, _vp, _vp, _vp, _sz, _vp, _i64, _i64, _i64, _i64, _i64, _int, _f32, _vp]),
+    "nn_fa_bwd_dq": (
+        _int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp, _i64, _i64, _i64, _i64, _i64, _int, _f32, _vp]
+    ),
     "nn_fa_last_error": (ctypes.c_char_p, []),
     "nn_fa_abi_version": (_int, []),
 }
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 
 @cache

@@ -74,7 +74,7 @@ def test_c_abi_rejects_misaligned_and_small_workspace():
     assert rc != 0 and "16-byte aligned" in L.nn_fa_last_error().decode()
     rc = L.nn_fa_bwd_dkdv(16, 16, 16, 16, 256, 10, 16, 16, 1, 4, 2, 16, 64, 1, 0.125, None)
     assert rc != 0 and "workspace too small" in L.nn_fa_last_error().decode()
-    rc = L.nn_fa_bwd_dq(16, 16, 16, 16, 256, 10, 16, 1, 4, 2, 16, 64, 1, 0.125, None)
+    rc = L.nn_fa_bwd_dq(16, 16, 16, 16, 16, 16, 256, 10, 16, 1, 4, 2, 16, 64, 1, 0.125, None)
     assert rc != 0 and "workspace too small" in L.nn_fa_last_error().decode()
     rc = L.nn_fa_bwd_pre(16, 16, 16, 0, 1 << 20, 1, 4, 2, 16, 64, 1, 0.125, None)
     assert rc != 0 and "null workspace" in L.nn_fa_last_error().decode()
