@@ -24,7 +24,9 @@ The JSON line also carries:
                 then the dK/dV kernel) and the HBM rate of the standalone preprocessing entry point;
   layout_fusion the same fwd+bwd from (B, T, heads, hd) projections: through transposed views and the
                 dense ops (the reference model's flow, with its copies) vs the layout-fused
-                nanonemo::flash_attn_bthd ops.
+                nanonemo::flash_attn_bthd ops;
+  rope_qk       the HIP RoPE kernel on the workload's q and k (projection layout, one launch) and its
+                HBM rate, beside the plain-PyTorch formula.
 """
 
 from __future__ import annotations
@@ -197,6 +199,17 @@ def main():
         for _ in range(args.steps):
             check(L.nn_fa_bwd_pre(ptr["o"], ptr["do"], ptr["lse"], ptr["ws"], ws_bytes, B, H, KVH, T, D, dt_code,
                                   scale, sp))
+        # The RoPE kernel on the workload's q and k in the projection layout.
+        from nanonemo_amd.kernels.hip import check_rope, strides3
+        from nanonemo_amd.model import rope_tables
+
+        qp, kp = q.transpose(1, 2).contiguous(), k.transpose(1, 2).contiguous()
+        qr, kr = torch.empty_like(qp), torch.empty_like(kp)
+        cos_t, sin_t = (t.to(dev) for t in rope_tables(D, T, 10000.0))
+        for _ in range(args.steps):
+            check_rope(L.nn_rope_qk(qp.data_ptr(), qr.data_ptr(), kp.data_ptr(), kr.data_ptr(), cos_t.data_ptr(),
+                                    sin_t.data_ptr(), B, T, H, KVH, D, strides3(T * H * D, H * D, D),
+                                    strides3(T * KVH * D, KVH * D, D), T, dt_code, sp))
         # A plain device copy of known size, for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE readings.
         src = torch.empty(COPY_CALIB_BYTES // 2, dtype=torch.bfloat16, device=dev).fill_(1.0)
         dst = torch.empty_like(src)
@@ -262,6 +275,32 @@ def main():
     views_ms = timed(step_views, args.steps)
     fused_ms = timed(step_fused, args.steps)
 
+    # ---- the RoPE kernel beside the op (q and k in the projection layout, one launch) ----
+    from nanonemo_amd.kernels.hip.rope import rope_qk
+    from nanonemo_amd.model import rope, rope_tables
+
+    from nanonemo_amd.kernels.hip import check_rope, strides3
+
+    cos_t, sin_t = (t.to(dev) for t in rope_tables(D, T, 10000.0))
+    for _ in range(5):
+        rope_qk(qp, kp, cos_t, sin_t)
+    rope_op_us = timed(lambda: rope_qk(qp, kp, cos_t, sin_t), max(20, args.steps)) * 1e3
+    torch_rope_us = timed(lambda: (rope(qp, cos_t, sin_t, 1), rope(kp, cos_t, sin_t, 1)), max(20, args.steps)) * 1e3
+    # the kernel alone: C-ABI launches with prepared arguments, events on the launch stream
+    qr, kr = torch.empty_like(qp), torch.empty_like(kp)
+    rope_args = (qp.data_ptr(), qr.data_ptr(), kp.data_ptr(), kr.data_ptr(), cos_t.data_ptr(), sin_t.data_ptr(),
+                 B, T, H, KVH, D, strides3(T * H * D, H * D, D), strides3(T * KVH * D, KVH * D, D), T, dt_code, sp)
+    for _ in range(5):
+        check_rope(L.nn_rope_qk(*rope_args))
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(200):
+        check_rope(L.nn_rope_qk(*rope_args))
+    e1.record(stream)
+    e1.synchronize()
+    rope_us = e0.elapsed_time(e1) * 1e3 / 200
+    rope_bytes = 2 * (qp.numel() + kp.numel()) * qp.element_size()  # read and write q and k
+
     e = 2  # bytes per 16-bit element
     pre_alg_bytes = 2 * B * H * T * D * e + 4 * B * H * T
     pre_all_bytes = pre_alg_bytes + 8 * B * H * T  # also reads lse and writes -lse/scale
@@ -308,6 +347,12 @@ def main():
         },
         "pct_of_bf16_peak": round(100 * value / PEAK_TFLOPS, 2),
         "op_ms_per_step": round(op_ms, 5),
+        "rope_qk": {
+            "kernel_us": round(rope_us, 2),
+            "GBps": round(rope_bytes / (rope_us * 1e-6) / 1e9, 1),
+            "op_us": round(rope_op_us, 2),
+            "torch_formula_us": round(torch_rope_us, 2),
+        },
         "layout_fusion": {
             "from": "projection layout (B, T, heads, hd)",
             "views_ms_per_step": round(views_ms, 5),

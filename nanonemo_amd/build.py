@@ -3,7 +3,7 @@
 Replaces the reference's JIT build (/root/reference/nanonemo/kernels/cuda/__init__.py:15-18, which runs
 nvcc through torch.utils.cpp_extension.load on first use): here ``hipcc`` compiles
 ``nanonemo_amd/csrc/*.hip`` once, in-tree, into ``nanonemo_amd/lib/libnanonemo_fa.so``, a plain C-ABI
-shared library with no torch types in its signatures (include/nanonemo_fa.h). The library is loaded
+shared library with no torch types in its signatures (include/nanonemo_fa.h, include/nanonemo_rope.h). The library is loaded
 with ctypes (nanonemo_amd/kernels/hip/__init__.py), so the same .so runs on any box with the ROCm
 runtime.
 
@@ -20,7 +20,7 @@ from pathlib import Path
 
 PKG = Path(__file__).resolve().parent
 ROOT = PKG.parent
-SRC = PKG / "csrc" / "flash_attn.hip"
+SRCS = [PKG / "csrc" / "flash_attn.hip", PKG / "csrc" / "rope.hip"]
 LIB_DIR = PKG / "lib"
 LIB = LIB_DIR / "libnanonemo_fa.so"
 ARCH = "gfx950"
@@ -56,7 +56,7 @@ def build(verbose: bool = False) -> Path:
     """Compile the HIP library (always recompiles) and return its path."""
     LIB_DIR.mkdir(parents=True, exist_ok=True)
     tmp = LIB.with_suffix(".so.tmp")
-    cmd = [hipcc(), *HIPCC_FLAGS, f"-I{ROOT / 'include'}", "-o", str(tmp), str(SRC)]
+    cmd = [hipcc(), *HIPCC_FLAGS, f"-I{ROOT / 'include'}", "-o", str(tmp), *(str(s) for s in SRCS)]
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)

@@ -19,6 +19,7 @@ LIB_PATH = Path(__file__).resolve().parents[2] / "lib" / "libnanonemo_fa.so"
 
 DTYPE_F16 = 0
 DTYPE_BF16 = 1
+DTYPE_F32 = 2  # nn_rope_* only
 
 _i64 = ctypes.c_int64
 _vp = ctypes.c_void_p
@@ -27,7 +28,7 @@ _f32 = ctypes.c_float
 _sz = ctypes.c_size_t
 _i64p = ctypes.POINTER(ctypes.c_int64)
 
-# name -> (restype, argtypes); must match include/nanonemo_fa.h
+# name -> (restype, argtypes); must match include/nanonemo_fa.h and include/nanonemo_rope.h
 SIGNATURES: dict[str, tuple] = {
     "nn_fa_fwd": (_int, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _int, _f32, _vp]),
     "nn_fa_fwd_strided": (
@@ -51,6 +52,16 @@ SIGNATURES: dict[str, tuple] = {
     ),
     "nn_fa_last_error": (ctypes.c_char_p, []),
     "nn_fa_abi_version": (_int, []),
+    # include/nanonemo_rope.h
+    "nn_rope_qk": (
+        _int,
+        [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64p, _i64p, _i64, _int, _vp],
+    ),
+    "nn_rope_qk_bwd": (
+        _int,
+        [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64p, _i64p, _i64, _int, _vp],
+    ),
+    "nn_rope_last_error": (ctypes.c_char_p, []),
 }
 
 ABI_VERSION = 6
@@ -80,7 +91,14 @@ def strides3(b: int, h: int, t: int) -> ctypes.Array:
 
 
 def check(rc: int) -> None:
-    """Raise RuntimeError with the library's message when an entry point returns non-zero."""
+    """Raise RuntimeError with the library's message when an nn_fa_* entry point returns non-zero."""
     if rc != 0:
         msg = lib().nn_fa_last_error().decode(errors="replace")
         raise RuntimeError(msg or f"nanonemo_fa call failed with code {rc}")
+
+
+def check_rope(rc: int) -> None:
+    """Raise RuntimeError with the library's message when an nn_rope_* entry point returns non-zero."""
+    if rc != 0:
+        msg = lib().nn_rope_last_error().decode(errors="replace")
+        raise RuntimeError(msg or f"nanonemo_rope call failed with code {rc}")

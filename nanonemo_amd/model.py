@@ -44,6 +44,7 @@ class ModelConfig:
     init_std: float = 0.02
     attn_backend: str = "math"  # SDPA backend of the "torch" attention
     attn_kernel: str = "torch"  # "torch" | "hip" | "hip_bthd"
+    rope_kernel: str = "torch"  # "torch" | "hip" (q and k rotated in one launch, nanonemo::rope_qk)
 
     def __post_init__(self):
         if self.d_model % self.n_heads:
@@ -56,6 +57,8 @@ class ModelConfig:
             raise ValueError(f"unknown attn_backend {self.attn_backend!r}")
         if self.attn_kernel not in ("torch", "hip", "hip_bthd"):
             raise ValueError(f"unknown attn_kernel {self.attn_kernel!r}")
+        if self.rope_kernel not in ("torch", "hip"):
+            raise ValueError(f"unknown rope_kernel {self.rope_kernel!r}")
 
     @property
     def head_dim(self) -> int:
@@ -117,17 +120,26 @@ class Attention(nn.Module):
             from nanonemo_amd.kernels.hip import flash_attn as fa  # registers the ops; raises without the library
 
             self._fa = fa
+        if cfg.rope_kernel == "hip":
+            from nanonemo_amd.kernels.hip.rope import rope_qk
+
+            self._rope_qk = rope_qk
 
     def forward(self, x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
         B, T, _ = x.shape
         q = self.wq(x).view(B, T, self.H, self.hd)
         k = self.wk(x).view(B, T, self.KVH, self.hd)
         v = self.wv(x).view(B, T, self.KVH, self.hd)
+        hip_rope = self.cfg.rope_kernel == "hip"
+        if hip_rope:  # in the projection layout, q and k in one launch
+            q, k = self._rope_qk(q, k, cos, sin)
         if self.cfg.attn_kernel == "hip_bthd":
-            q, k = rope(q, cos, sin, seq_dim=1), rope(k, cos, sin, seq_dim=1)
+            if not hip_rope:
+                q, k = rope(q, cos, sin, seq_dim=1), rope(k, cos, sin, seq_dim=1)
             return self.wo(self._fa.flash_attn_bthd(q, k, v).view(B, T, -1))
         q, k, v = q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2)  # (B, heads, T, hd) views
-        q, k = rope(q, cos, sin, seq_dim=2), rope(k, cos, sin, seq_dim=2)
+        if not hip_rope:
+            q, k = rope(q, cos, sin, seq_dim=2), rope(k, cos, sin, seq_dim=2)
         if self.cfg.attn_kernel == "hip":
             y = self._fa.flash_attn(q, k, v)
         else:

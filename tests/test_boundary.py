@@ -13,12 +13,15 @@ import torch
 from nanonemo_amd.kernels.hip import ABI_VERSION, LIB_PATH, SIGNATURES, lib
 
 ROOT = Path(__file__).resolve().parents[1]
-HEADER = ROOT / "include" / "nanonemo_fa.h"
+HEADERS = sorted((ROOT / "include").glob("*.h"))
 
 
 def _declared_symbols() -> list[str]:
-    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
-    return sorted(set(re.findall(r"\b(nn_fa_\w+)\s*\(", text)))
+    names = set()
+    for h in HEADERS:
+        text = re.sub(r"/\*.*?\*/", "", h.read_text(), flags=re.S)
+        names |= set(re.findall(r"\b(nn_\w+)\s*\(", text))
+    return sorted(names)
 
 
 def test_library_is_built():
@@ -30,7 +33,7 @@ def test_library_exports_every_header_symbol():
     declared = _declared_symbols()
     assert declared, "no declarations parsed from the header"
     for name in declared:
-        assert hasattr(handle, name), f"{name} declared in {HEADER.name} but not exported"
+        assert hasattr(handle, name), f"{name} declared in include/ but not exported"
     # and the Python binding declares a signature for each of them
     assert sorted(SIGNATURES) == declared
 
@@ -101,6 +104,31 @@ def test_strided_c_abi_rejects_bad_strides_before_any_launch(qs, ks, msg):
     assert rc != 0 and msg in L.nn_fa_last_error().decode()
     rc = L.nn_fa_fwd_strided(16, 16, 16, 16, 16, B, H, KVH, T, D, None, strides3(*ks), 1, 0.125, None)
     assert rc != 0 and "null strides" in L.nn_fa_last_error().decode()
+
+
+@pytest.mark.parametrize(
+    "kw, msg",
+    [
+        (dict(D=56), "head_dim must be a multiple of 16"),
+        (dict(dtype=5), "dtype must be float16, bfloat16 or float32"),
+        (dict(T=40), "exceeds the 32 rows of the tables"),
+        (dict(qs=(4096, 768, 60)), "q strides must be positive multiples of 8"),
+        (dict(qp=24), "q must be 16-byte aligned"),
+        (dict(cosp=None), "null table"),
+    ],
+)
+def test_rope_c_abi_rejects_bad_arguments_before_any_launch(kw, msg):
+    from nanonemo_amd.kernels.hip import strides3
+
+    L = lib()
+    a = dict(D=64, dtype=1, T=16, qs=(4096, 768, 64), qp=16, cosp=256)
+    a.update(kw)
+    rc = L.nn_rope_qk(a["qp"], 32, 64, 96, a["cosp"], 512, 1, a["T"], 12, 4, a["D"], strides3(*a["qs"]),
+                      strides3(1024, 256, 64), 32, a["dtype"], None)
+    assert rc != 0 and msg in L.nn_rope_last_error().decode()
+    rc = L.nn_rope_qk_bwd(a["qp"], 32, 64, 96, a["cosp"], 512, 1, a["T"], 12, 4, a["D"], strides3(*a["qs"]),
+                          strides3(1024, 256, 64), 32, a["dtype"], None)
+    assert rc != 0 and msg in L.nn_rope_last_error().decode()
 
 
 def test_c_abi_empty_problem_is_a_no_op():
