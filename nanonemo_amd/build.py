@@ -3,7 +3,7 @@
 Replaces the reference's JIT build (/root/reference/nanonemo/kernels/cuda/__init__.py:15-18, which runs
 nvcc through torch.utils.cpp_extension.load on first use): here ``hipcc`` compiles
 ``nanonemo_amd/csrc/*.hip`` once, in-tree, into ``nanonemo_amd/lib/libnanonemo_fa.so``, a plain C-ABI
-shared library with no torch types in its signatures (include/nanonemo_fa.h, include/nanonemo_rope.h). The library is loaded
+shared library with no torch types in its signatures (include/nanonemo_fa.h, include/nanonemo_rope.h, include/nanonemo_rmsnorm.h). The library is loaded
 with ctypes (nanonemo_amd/kernels/hip/__init__.py), so the same .so runs on any box with the ROCm
 runtime.
 
@@ -20,7 +20,7 @@ from pathlib import Path
 
 PKG = Path(__file__).resolve().parent
 ROOT = PKG.parent
-SRCS = [PKG / "csrc" / "flash_attn.hip", PKG / "csrc" / "rope.hip"]
+SRCS = [PKG / "csrc" / "flash_attn.hip", PKG / "csrc" / "rope.hip", PKG / "csrc" / "rmsnorm.hip"]
 LIB_DIR = PKG / "lib"
 LIB = LIB_DIR / "libnanonemo_fa.so"
 ARCH = "gfx950"

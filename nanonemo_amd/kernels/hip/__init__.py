@@ -28,7 +28,7 @@ _f32 = ctypes.c_float
 _sz = ctypes.c_size_t
 _i64p = ctypes.POINTER(ctypes.c_int64)
 
-# name -> (restype, argtypes); must match include/nanonemo_fa.h and include/nanonemo_rope.h
+# name -> (restype, argtypes); must match include/nanonemo_fa.h, nanonemo_rope.h and nanonemo_rmsnorm.h
 SIGNATURES: dict[str, tuple] = {
     "nn_fa_fwd": (_int, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _int, _f32, _vp]),
     "nn_fa_fwd_strided": (
@@ -62,6 +62,13 @@ SIGNATURES: dict[str, tuple] = {
         [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64p, _i64p, _i64, _int, _vp],
     ),
     "nn_rope_last_error": (ctypes.c_char_p, []),
+    # include/nanonemo_rmsnorm.h
+    "nn_add_rmsnorm_fwd": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _f32, _int, _int, _int, _vp]),
+    "nn_add_rmsnorm_bwd_workspace_size": (_sz, [_i64, _i64]),
+    "nn_add_rmsnorm_bwd": (
+        _int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _i64, _i64, _int, _int, _int, _int, _vp]
+    ),
+    "nn_rmsnorm_last_error": (ctypes.c_char_p, []),
 }
 
 ABI_VERSION = 6
@@ -102,3 +109,10 @@ def check_rope(rc: int) -> None:
     if rc != 0:
         msg = lib().nn_rope_last_error().decode(errors="replace")
         raise RuntimeError(msg or f"nanonemo_rope call failed with code {rc}")
+
+
+def check_rmsnorm(rc: int) -> None:
+    """Raise RuntimeError with the library's message when an nn_add_rmsnorm_* entry point returns non-zero."""
+    if rc != 0:
+        msg = lib().nn_rmsnorm_last_error().decode(errors="replace")
+        raise RuntimeError(msg or f"nanonemo_rmsnorm call failed with code {rc}")

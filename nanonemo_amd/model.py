@@ -13,8 +13,10 @@ tied input/output embedding, GPT-2 style init with the residual projections scal
              "cuda" setting, layers.py:89-93,106-108, including its transposes and copies);
   * "hip_bthd": the layout-fused op nanonemo::flash_attn_bthd, which reads the projections and RoPE
              output in their (B, T, heads, hd) layout and writes o where the output projection reads it.
-Only the attention is this build's; the rest is plain PyTorch (the reference's other kernels are out
-of scope here).
+``rope_kernel="hip"`` rotates q and k with this build's RoPE kernel (nanonemo::rope_qk) and
+``norm_kernel="hip"`` runs the residual add + RMSNorm on either side of attention as this build's fused
+kernel (nanonemo::cuda_add_rms_norm_fwd / _bwd, the reference's norm_kernel="cuda"); everything else
+is plain PyTorch.
 """
 
 from __future__ import annotations
@@ -45,6 +47,7 @@ class ModelConfig:
     attn_backend: str = "math"  # SDPA backend of the "torch" attention
     attn_kernel: str = "torch"  # "torch" | "hip" | "hip_bthd"
     rope_kernel: str = "torch"  # "torch" | "hip" (q and k rotated in one launch, nanonemo::rope_qk)
+    norm_kernel: str = "torch"  # "torch" | "hip" (fused residual add + RMSNorm, nanonemo::cuda_add_rms_norm_*)
 
     def __post_init__(self):
         if self.d_model % self.n_heads:
@@ -59,6 +62,8 @@ class ModelConfig:
             raise ValueError(f"unknown attn_kernel {self.attn_kernel!r}")
         if self.rope_kernel not in ("torch", "hip"):
             raise ValueError(f"unknown rope_kernel {self.rope_kernel!r}")
+        if self.norm_kernel not in ("torch", "hip"):
+            raise ValueError(f"unknown norm_kernel {self.norm_kernel!r}")
 
     @property
     def head_dim(self) -> int:
@@ -79,9 +84,20 @@ class RMSNorm(nn.Module):
 
 
 class AddRMSNorm(RMSNorm):
-    """(rmsnorm(x + delta), x + delta): the pending sublayer output joins the stream here (layers.py:36-56)."""
+    """(rmsnorm(x + delta), x + delta): the pending sublayer output joins the stream here (layers.py:36-56).
+    kernel="hip" does both in one pass with this build's fused kernel."""
+
+    def __init__(self, dim: int, eps: float, kernel: str = "torch"):
+        super().__init__(dim, eps)
+        self.fused = None
+        if kernel == "hip":
+            from nanonemo_amd.kernels.hip.rmsnorm import add_rms_norm  # raises without the library
+
+            self.fused = add_rms_norm
 
     def forward(self, x: torch.Tensor, delta: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+        if self.fused is not None:
+            return self.fused(x, delta, self.weight, self.eps)
         if delta is not None:
             x = x + delta
         return super().forward(x), x
@@ -170,9 +186,9 @@ class Block(nn.Module):
 
     def __init__(self, cfg: ModelConfig):
         super().__init__()
-        self.norm_attn = AddRMSNorm(cfg.d_model, cfg.norm_eps)
+        self.norm_attn = AddRMSNorm(cfg.d_model, cfg.norm_eps, cfg.norm_kernel)
         self.attn = Attention(cfg)
-        self.norm_mlp = AddRMSNorm(cfg.d_model, cfg.norm_eps)
+        self.norm_mlp = AddRMSNorm(cfg.d_model, cfg.norm_eps, cfg.norm_kernel)
         self.mlp = MLP(cfg)
 
     def forward(self, x, cos, sin, delta=None):
@@ -189,7 +205,7 @@ class NanoNemo(nn.Module):
         self.cfg = cfg
         self.tok_emb = nn.Embedding(cfg.vocab_size, cfg.d_model)
         self.blocks = nn.ModuleList(Block(cfg) for _ in range(cfg.n_layers))
-        self.norm_out = AddRMSNorm(cfg.d_model, cfg.norm_eps)
+        self.norm_out = AddRMSNorm(cfg.d_model, cfg.norm_eps, cfg.norm_kernel)
         self.lm_head = nn.Linear(cfg.d_model, cfg.vocab_size, bias=False)
         self.lm_head.weight = self.tok_emb.weight
         cos, sin = rope_tables(cfg.head_dim, cfg.max_seq_len, cfg.rope_base)

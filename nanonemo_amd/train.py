@@ -63,10 +63,14 @@ def make_optimizer(model, lr: float = 6e-4):
 def run(attn: str, steps: int, batch: int, seq: int, cfg_kwargs: dict, device: str = "cuda", warmup: int = 3):
     """Train ``steps`` steps from the seed-0 init on the seed-0 synthetic stream; returns the per-step
     losses and the tokens/s over the steps after ``warmup``. ``attn`` is an attn_kernel, optionally
-    with a "+rope" suffix for rope_kernel="hip"."""
+    with "+rope" (rope_kernel="hip") and "+norm" (norm_kernel="hip") suffixes."""
     torch.manual_seed(0)
-    kernel, _, extra = attn.partition("+")
-    model = NanoNemo(ModelConfig(**cfg_kwargs, attn_kernel=kernel, rope_kernel="hip" if extra == "rope" else "torch")).to(device)
+    kernel, *extras = attn.split("+")
+    unknown = set(extras) - {"rope", "norm"}
+    if unknown:
+        raise ValueError(f"unknown kernel suffixes {sorted(unknown)}")
+    model = NanoNemo(ModelConfig(**cfg_kwargs, attn_kernel=kernel, rope_kernel="hip" if "rope" in extras else "torch",
+                                 norm_kernel="hip" if "norm" in extras else "torch")).to(device)
     opt = make_optimizer(model)
     data = synthetic_batches(steps, batch, seq, model.cfg.vocab_size, device)
     losses = []
@@ -88,8 +92,8 @@ def main():
     p.add_argument("--steps", type=int, default=50)
     p.add_argument("--batch", type=int, default=8)
     p.add_argument("--seq", type=int, default=1024)
-    p.add_argument("--attn", nargs="+", default=["torch", "hip", "hip_bthd", "hip_bthd+rope"],
-                   help="attention kernels; a '+rope' suffix also selects the HIP RoPE kernel")
+    p.add_argument("--attn", nargs="+", default=["torch", "hip", "hip_bthd", "hip_bthd+rope", "hip_bthd+rope+norm"],
+                   help="attention kernels; '+rope' / '+norm' suffixes also select the HIP RoPE / add+RMSNorm kernels")
     p.add_argument("--small", action="store_true", help="a 2-layer model (quick check)")
     a = p.parse_args()
     cfg_kwargs = dict(n_layers=2, d_model=256, n_heads=4, n_kv_heads=2, d_ff=512, vocab_size=512, max_seq_len=a.seq) \

@@ -131,6 +131,72 @@ def test_rope_c_abi_rejects_bad_arguments_before_any_launch(kw, msg):
     assert rc != 0 and msg in L.nn_rope_last_error().decode()
 
 
+@pytest.mark.parametrize(
+    "kw, msg",
+    [
+        (dict(N=4100), "hidden size must be <= 1024, or a multiple of 8 and <= 4096"),
+        (dict(N=4104), "hidden size must be <= 1024, or a multiple of 8 and <= 4096"),
+        (dict(N=0), "invalid sizes"),
+        (dict(M=-1), "invalid sizes"),
+        (dict(xdt=3), "dtype must be float16, bfloat16 or float32"),
+        (dict(x=24), "tensors must be 16-byte aligned"),
+        (dict(x=None), "null pointer argument"),
+        (dict(eps=-1.0), "eps must be non-negative"),
+    ],
+)
+def test_rmsnorm_c_abi_rejects_bad_arguments_before_any_launch(kw, msg):
+    L = lib()
+    a = dict(M=16, N=768, x=256, xdt=2, eps=1e-5)
+    a.update(kw)
+    rc = L.nn_add_rmsnorm_fwd(a["x"], 512, 1024, 2048, 4096, 8192, a["M"], a["N"], a["eps"], a["xdt"], 1, 1, None)
+    assert rc != 0 and msg in L.nn_rmsnorm_last_error().decode()
+
+
+def test_rmsnorm_c_abi_backward_checks_and_workspace():
+    L = lib()
+    # one fp32 dw row per block (a block takes 8 rows, 2 per wave, for N <= 2048 with N % 8 == 0, else 4;
+    # at most 1024 blocks), plus one row per 64-row slice of those when there is more than one slice
+    assert L.nn_add_rmsnorm_bwd_workspace_size(8192, 768) == (1024 + 16) * 768 * 4
+    assert L.nn_add_rmsnorm_bwd_workspace_size(7, 768) == 1 * 768 * 4
+    assert L.nn_add_rmsnorm_bwd_workspace_size(7, 4096) == 2 * 4096 * 4
+    assert L.nn_add_rmsnorm_bwd_workspace_size(520, 768) == (65 + 2) * 768 * 4
+    assert L.nn_add_rmsnorm_bwd_workspace_size(1 << 20, 33) == (1024 + 16) * 33 * 4
+    assert L.nn_add_rmsnorm_bwd_workspace_size(0, 768) == 0
+    args = (256, 512, 768, 1024, 2048, 4096, 8192, 16384)
+    rc = L.nn_add_rmsnorm_bwd(*args, 32768, 10, 64, 768, 1, 2, 2, 1, None)
+    assert rc != 0 and "workspace too small" in L.nn_rmsnorm_last_error().decode()
+    rc = L.nn_add_rmsnorm_bwd(*args, None, 1 << 20, 64, 768, 1, 2, 2, 1, None)
+    assert rc != 0 and "null workspace" in L.nn_rmsnorm_last_error().decode()
+    rc = L.nn_add_rmsnorm_bwd(*args, 32768, 1 << 20, 64, 768, 1, 9, 2, 1, None)
+    assert rc != 0 and "dtype" in L.nn_rmsnorm_last_error().decode()
+
+
+def test_rmsnorm_ops_registered_with_reference_schemas():
+    from nanonemo_amd.kernels.hip import rmsnorm  # noqa: F401
+
+    fwd = str(torch.ops.nanonemo.cuda_add_rms_norm_fwd.default._schema)
+    bwd = str(torch.ops.nanonemo.cuda_add_rms_norm_bwd.default._schema)
+    assert fwd == ("nanonemo::cuda_add_rms_norm_fwd(Tensor x, Tensor? delta, Tensor weight, float eps, "
+                   "ScalarType out_dtype) -> (Tensor, Tensor, Tensor)")
+    assert bwd == ("nanonemo::cuda_add_rms_norm_bwd(Tensor dy, Tensor? dh, Tensor h, Tensor weight, Tensor rstd, "
+                   "ScalarType dx_dtype, ScalarType? ddelta_dtype) -> (Tensor, Tensor, Tensor)")
+
+
+def test_rmsnorm_fakes_follow_the_reference():
+    from nanonemo_amd.kernels.hip import rmsnorm  # noqa: F401
+
+    x = torch.empty(4, 16, 768, device="meta")
+    d = torch.empty(4, 16, 768, dtype=torch.bfloat16, device="meta")
+    w = torch.empty(768, device="meta")
+    y, h, rstd = torch.ops.nanonemo.cuda_add_rms_norm_fwd(x, d, w, 1e-5, torch.bfloat16)
+    assert y.dtype == torch.bfloat16 and h.dtype == torch.float32 and rstd.shape == (4, 16) and y.shape == x.shape
+    y, h, _ = torch.ops.nanonemo.cuda_add_rms_norm_fwd(x, None, w, 1e-5, torch.float32)
+    assert h.numel() == 0
+    dx, dd, dw = torch.ops.nanonemo.cuda_add_rms_norm_bwd(y, h.new_empty(x.shape), x, w, rstd, torch.float32,
+                                                          torch.bfloat16)
+    assert dx.dtype == torch.float32 and dd.dtype == torch.bfloat16 and dw.shape == w.shape
+
+
 def test_c_abi_empty_problem_is_a_no_op():
     # T == 0 and B == 0 return success without touching device memory (flash_attn.cu:367).
     L = lib()

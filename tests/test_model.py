@@ -102,3 +102,9 @@ def test_train_step_on_torch_attention():
 def test_unknown_attention_kernel_is_rejected():
     with pytest.raises(ValueError):
         ModelConfig(attn_kernel="cuda_v2")
+
+
+@pytest.mark.parametrize("field", ["rope_kernel", "norm_kernel"])
+def test_unknown_neighbour_kernel_is_rejected(field):
+    with pytest.raises(ValueError):
+        ModelConfig(**{field: "triton"})

@@ -17,9 +17,11 @@ SMALL = dict(n_layers=2, d_model=256, n_heads=4, n_kv_heads=2, d_ff=512, vocab_s
 
 
 def _pair(attn: str):
+    """The plain model and one with this build's kernels ("+norm": also the fused add + RMSNorm)."""
+    kernel, *extras = attn.split("+")
     torch.manual_seed(0)
     ref = NanoNemo(ModelConfig(**SMALL)).cuda()
-    fast = NanoNemo(ModelConfig(**SMALL, attn_kernel=attn)).cuda()
+    fast = NanoNemo(ModelConfig(**SMALL, attn_kernel=kernel, norm_kernel="hip" if "norm" in extras else "torch")).cuda()
     fast.load_state_dict(ref.state_dict())
     idx = torch.randint(0, SMALL["vocab_size"], (2, 128), device="cuda")
     return ref, fast, idx, torch.roll(idx, -1, dims=1)
@@ -29,7 +31,7 @@ def _grads(model):
     return {n: p.grad for n, p in model.named_parameters()}
 
 
-@pytest.mark.parametrize("attn", ["hip", "hip_bthd"])
+@pytest.mark.parametrize("attn", ["hip", "hip_bthd", "hip_bthd+norm"])
 def test_bf16_autocast_loss_and_grads_match_torch_attention(attn):
     print(f"\n[case] model {attn} vs torch attention, bf16 autocast", flush=True)
     ref, fast, idx, tgt = _pair(attn)
@@ -87,3 +89,20 @@ def test_short_training_run_tracks_torch_attention():
     torch.testing.assert_close(curves["hip_bthd"][:5], curves["torch"][:5], rtol=0, atol=2e-2)
     torch.testing.assert_close(curves["hip_bthd"], curves["torch"], rtol=5e-2, atol=0)
     assert curves["hip_bthd"][-1] < curves["hip_bthd"][0] - 0.5
+
+
+def test_fused_norm_model_tracks_the_plain_norm_model():
+    # The whole model with the fused add + RMSNorm (and the layout-fused attention) against the same model
+    # with plain-PyTorch norms, bf16 autocast: the norms' outputs differ only in rounding order.
+    _, a, idx, tgt = _pair("hip_bthd")
+    torch.manual_seed(0)
+    b = NanoNemo(ModelConfig(**SMALL, attn_kernel="hip_bthd", norm_kernel="hip")).cuda()
+    b.load_state_dict(a.state_dict())
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        la = a(idx, tgt)[1]
+        lb = b(idx, tgt)[1]
+    la.backward()
+    lb.backward()
+    torch.testing.assert_close(lb, la, rtol=2e-3, atol=2e-3)
+    for (n, ga), gb in zip(_grads(a).items(), _grads(b).values()):
+        torch.testing.assert_close(gb, ga, rtol=5e-2, atol=5e-2 * ga.abs().max().item(), msg=n)
