@@ -26,7 +26,10 @@ The JSON line also carries:
                 dense ops (the reference model's flow, with its copies) vs the layout-fused
                 nanonemo::flash_attn_bthd ops;
   rope_qk       the HIP RoPE kernel on the workload's q and k (projection layout, one launch) and its
-                HBM rate, beside the plain-PyTorch formula.
+                HBM rate, beside the plain-PyTorch formula;
+  add_rmsnorm   the HIP fused residual add + RMSNorm forward and backward (dx, ddelta and dw) on the
+                114 M model's stream at this workload's tokens (B*T rows of 768, fp32 residual, bf16
+                sublayer output and normalised output) and their HBM rates.
 """
 
 from __future__ import annotations
@@ -49,6 +52,45 @@ METRIC = "causal GQA attn fwd+bwd TFLOP/s at T=1024; % of BF16 MFMA peak"
 PEAK_TFLOPS = 2500.0  # MI355X dense BF16/FP16 MFMA, published
 PEAK_HBM_GBPS = 8000.0
 COPY_CALIB_BYTES = 256 << 20  # size of the calibration copy run by --profile-only
+
+
+NORM_D = 768  # d_model of the 114 M model
+
+
+def _norm_launches(L, M, dev, sp):
+    """C-ABI launches of the fused add + RMSNorm on M rows of the model's residual stream (fp32 x, bf16
+    delta and output, fp32 weight), with their algorithmic HBM bytes."""
+    import torch
+
+    from nanonemo_amd.kernels.hip import check_rmsnorm
+
+    N = NORM_D
+    g = torch.Generator(device=dev).manual_seed(1)
+    x = torch.randn(M, N, device=dev, generator=g)
+    d = torch.randn(M, N, device=dev, generator=g).bfloat16()
+    w = torch.ones(N, device=dev)
+    y = torch.empty(M, N, device=dev, dtype=torch.bfloat16)
+    h = torch.empty(M, N, device=dev)
+    rstd = torch.empty(M, device=dev)
+    dy = torch.randn(M, N, device=dev, generator=g).bfloat16()
+    dh = torch.randn(M, N, device=dev, generator=g)
+    dx = torch.empty(M, N, device=dev)
+    dd = torch.empty(M, N, device=dev, dtype=torch.bfloat16)
+    dw = torch.empty(N, device=dev)
+    wsb = L.nn_add_rmsnorm_bwd_workspace_size(M, N)
+    ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=dev)
+    keep = (x, d, w, y, h, rstd, dy, dh, dx, dd, dw, ws)
+    return {
+        "fwd": lambda: check_rmsnorm(L.nn_add_rmsnorm_fwd(x.data_ptr(), d.data_ptr(), w.data_ptr(), y.data_ptr(),
+                                                          h.data_ptr(), rstd.data_ptr(), M, N, 1e-5, 2, 1, 1, sp)),
+        "bwd": lambda: check_rmsnorm(L.nn_add_rmsnorm_bwd(dy.data_ptr(), dh.data_ptr(), h.data_ptr(), w.data_ptr(),
+                                                          rstd.data_ptr(), dx.data_ptr(), dd.data_ptr(), dw.data_ptr(),
+                                                          ws.data_ptr(), wsb, M, N, 1, 2, 2, 1, sp)),
+        # read x, delta; write h, y, rstd  |  read dy, dh, h, rstd; write dx, ddelta (dw and its partials aside)
+        "fwd_bytes": M * N * (4 + 2 + 4 + 2) + 4 * M,
+        "bwd_bytes": M * N * (2 + 4 + 4 + 4 + 2) + 4 * M,
+        "keep": keep,
+    }
 
 
 def parse():
@@ -210,6 +252,11 @@ def main():
             check_rope(L.nn_rope_qk(qp.data_ptr(), qr.data_ptr(), kp.data_ptr(), kr.data_ptr(), cos_t.data_ptr(),
                                     sin_t.data_ptr(), B, T, H, KVH, D, strides3(T * H * D, H * D, D),
                                     strides3(T * KVH * D, KVH * D, D), T, dt_code, sp))
+        # The fused add + RMSNorm, forward and backward, on the model's residual stream at these tokens.
+        norm = _norm_launches(L, B * T, dev, sp)
+        for _ in range(args.steps):
+            norm["fwd"]()
+            norm["bwd"]()
         # A plain device copy of known size, for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE readings.
         src = torch.empty(COPY_CALIB_BYTES // 2, dtype=torch.bfloat16, device=dev).fill_(1.0)
         dst = torch.empty_like(src)
@@ -301,6 +348,20 @@ def main():
     rope_us = e0.elapsed_time(e1) * 1e3 / 200
     rope_bytes = 2 * (qp.numel() + kp.numel()) * qp.element_size()  # read and write q and k
 
+    # ---- the fused add + RMSNorm on the model's residual stream (B*T rows of d_model) ----
+    norm = _norm_launches(L, B * T, dev, sp)
+    norm_us = {}
+    for name in ("fwd", "bwd"):
+        for _ in range(5):
+            norm[name]()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(200):
+            norm[name]()
+        e1.record(stream)
+        e1.synchronize()
+        norm_us[name] = e0.elapsed_time(e1) * 1e3 / 200
+
     e = 2  # bytes per 16-bit element
     pre_alg_bytes = 2 * B * H * T * D * e + 4 * B * H * T
     pre_all_bytes = pre_alg_bytes + 8 * B * H * T  # also reads lse and writes -lse/scale
@@ -352,6 +413,13 @@ def main():
             "GBps": round(rope_bytes / (rope_us * 1e-6) / 1e9, 1),
             "op_us": round(rope_op_us, 2),
             "torch_formula_us": round(torch_rope_us, 2),
+        },
+        "add_rmsnorm": {
+            "shape": f"{B * T} x {NORM_D}, x fp32 + delta bf16 -> y bf16, h fp32",
+            "fwd_us": round(norm_us["fwd"], 2),
+            "fwd_GBps": round(norm["fwd_bytes"] / (norm_us["fwd"] * 1e-6) / 1e9, 1),
+            "bwd_us": round(norm_us["bwd"], 2),
+            "bwd_GBps": round(norm["bwd_bytes"] / (norm_us["bwd"] * 1e-6) / 1e9, 1),
         },
         "layout_fusion": {
             "from": "projection layout (B, T, heads, hd)",
