@@ -223,6 +223,13 @@ __device__ inline void wait_vmem_keep() {
     __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
 }
 
+// Block barrier that orders LDS only: this wave's LDS accesses complete, then s_barrier. Vector-memory
+// operations (global loads and stores, LDS DMA) may stay in flight across it, so it must only be used
+// where no wave reads, before its own vmcnt wait, LDS that such an operation writes. (__syncthreads
+// also waits for every vector-memory operation.) The memory clobber keeps the compiler from moving
+// memory accesses across it.
+__device__ inline void barrier_lds() { __asm__ volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 // The other half-wave's value combined with this lane's: v_permlane32_swap exchanges the two
 // 32-lane halves, and its two results hold this lane's value and its partner's (lane ^ 32).
 __device__ inline float pair_max(float x) {
@@ -485,7 +492,7 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(
     constexpr int QT = BM * HD;  // elements of one Q or dO tile
     constexpr int CH4 = HD / 4;  // 16-byte fp32 chunks per staged gradient row
     static_assert(BNK == BM, "a unit's first query tile is its own index");
-    static_assert(2 * NW * QT * 2 * 2 >= NW * 2 * BNK * HD * 4, "gradient staging fits in the tile space");
+    static_assert(2 * NW * QT * 2 >= NW * BNK * HD * 4, "one gradient's staging fits in the B tile buffers");
     __shared__ __attribute__((aligned(16))) u16 qA[NW * QT];
     __shared__ __attribute__((aligned(16))) u16 oA[NW * QT];
     __shared__ __attribute__((aligned(16))) u16 qB[NW * QT];
@@ -511,47 +518,57 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(
 #pragma unroll
         for (int x = 0; x < 2; ++x) qcoff[dt][x] = col_off<HD>(8 * x + 4 * hh, 32 * dt + 16 * g16, lane);
 
-    for (int ui = 0; ui < 2; ++ui) {
-        const int unit = ui == 0 ? pj : nkb - 1 - pj;
-        if (ui == 1 && unit <= pj) break;  // an odd unit count leaves the middle unit alone
-        const int kb0 = unit * BNK;
-        const int qt_first = unit, nq = nqt - qt_first, niter = group * nq;
-        const int nmine = wave < niter ? (niter - wave + NW - 1) / NW : 0;  // iterations wave, wave+NW, ...
-
-        u16x8 kf[NSL][NS], vf[NSL][NS];
+    // A unit's K / V operands (every wave holds all 64 keys).
+    u16x8 kf[NSL][NS], vf[NSL][NS];
+    auto load_kv = [&](int kb0_) {
 #pragma unroll
         for (int sl = 0; sl < NSL; ++sl) {
-            const int key = min(kb0 + 32 * sl + l32, T - 1);  // keys past T are masked below
+            const int key = min(kb0_ + 32 * sl + l32, T - 1);  // keys past T are masked below
 #pragma unroll
             for (int s = 0; s < NS; ++s) {
                 kf[sl][s] = ld8(K + kvoff + (size_t)key * lk.st + 16 * s + 8 * hh);
                 vf[sl][s] = ld8(V + kvoff + (size_t)key * lk.st + 16 * s + 8 * hh);
             }
         }
+    };
+    // DMA iteration itn of the unit whose query tiles start at tile qtf (nqq of them: iteration itn is
+    // query head itn / nqq of the group, tile qtf + itn % nqq) into this wave's slot: the Q / dO tiles
+    // and the -lse/scale, -D vectors.
+    auto issue_it = [&](int itn, int qtf, int nqq, u16* qs, u16* os, float* ls) {
+        // Wave-uniform in fact; made uniform for the compiler only here, so that the tile addressing is
+        // scalar without keeping scalar copies alive across the whole kernel.
+        const int itu = __builtin_amdgcn_readfirstlane(itn), wu = __builtin_amdgcn_readfirstlane(wave);
+        const int hq = kvh * group + itu / nqq;
+        const size_t ro = ((size_t)b * H + hq) * T;  // first row of the head's [T] vectors
+        const size_t qo = lq.at(b, hq);
+        const int q0 = (qtf + itu % nqq) * BM;
+        dma_rows<HD, BM, 1>(Q + qo, lq.st, q0, T, qs + wu * QT, 0, dl);
+        dma_rows<HD, BM, 1>(dO + qo, lq.st, q0, T, os + wu * QT, 0, dl);
+        const uint32_t lo = (uint32_t)min(lane, T - 1 - q0) * 4;  // rows past T repeat row T - 1
+        __builtin_amdgcn_global_load_lds(reinterpret_cast<const char*>(nLvec + ro + q0) + lo, LDS_AS(void, ls + wu * 2 * BM), 4, 0, 0);
+        __builtin_amdgcn_global_load_lds(reinterpret_cast<const char*>(nDvec + ro + q0) + lo, LDS_AS(void, ls + wu * 2 * BM + BM), 4, 0, 0);
+    };
+    // The first unit's K / V and first tiles; each later unit's are issued before the previous unit's
+    // reduction, so that their latency overlaps it.
+    const int nunits = nkb - 1 - pj > pj ? 2 : 1;  // an odd unit count leaves the middle unit alone
+    load_kv(pj * BNK);
+    if (wave < group * (nqt - pj)) issue_it(wave, pj, nqt - pj, qA, oA, lA);
+
+    for (int ui = 0; ui < nunits; ++ui) {
+        const int unit = ui == 0 ? pj : nkb - 1 - pj;
+        const int kb0 = unit * BNK;
+        const int qt_first = unit, nq = nqt - qt_first, niter = group * nq;
+        const int nmine = wave < niter ? (niter - wave + NW - 1) / NW : 0;  // iterations wave, wave+NW, ...
+
         f32x16 dk[NSL][ND], dv[NSL][ND];
 #pragma unroll
         for (int sl = 0; sl < NSL; ++sl)
 #pragma unroll
             for (int dt = 0; dt < ND; ++dt) dk[sl][dt] = dv[sl][dt] = f32x16{};
 
-        // Iteration itn -> (query head of the group, 64-row query tile).
+        // Iteration itn -> 64-row query tile.
         auto qbase_of = [&](int itn) { return (qt_first + itn % nq) * BM; };
-        auto head_of = [&](int itn) { return kvh * group + itn / nq; };
-        // DMA iteration itn's Q / dO tiles and -lse/scale, -D vectors into this wave's slot.
-        auto issue = [&](int itn, u16* qs, u16* os, float* ls) {
-            // Wave-uniform in fact; made uniform for the compiler only here, so that the tile
-            // addressing is scalar without keeping scalar copies alive across the whole kernel.
-            const int itu = __builtin_amdgcn_readfirstlane(itn), wu = __builtin_amdgcn_readfirstlane(wave);
-            const int hq = head_of(itu);
-            const size_t ro = ((size_t)b * H + hq) * T;  // first row of the head's [T] vectors
-            const size_t qo = lq.at(b, hq);
-            const int q0 = qbase_of(itu);
-            dma_rows<HD, BM, 1>(Q + qo, lq.st, q0, T, qs + wu * QT, 0, dl);
-            dma_rows<HD, BM, 1>(dO + qo, lq.st, q0, T, os + wu * QT, 0, dl);
-            const uint32_t lo = (uint32_t)min(lane, T - 1 - q0) * 4;  // rows past T repeat row T - 1
-            __builtin_amdgcn_global_load_lds(reinterpret_cast<const char*>(nLvec + ro + q0) + lo, LDS_AS(void, ls + wu * 2 * BM), 4, 0, 0);
-            __builtin_amdgcn_global_load_lds(reinterpret_cast<const char*>(nDvec + ro + q0) + lo, LDS_AS(void, ls + wu * 2 * BM + BM), 4, 0, 0);
-        };
+        auto issue = [&](int itn, u16* qs, u16* os, float* ls) { issue_it(itn, qt_first, nq, qs, os, ls); };
         // One 64-query iteration: two 32-query steps, each against both 32-key slabs.
         // MASK: the iteration crosses the diagonal or T (a separate instantiation, so that unmasked
         // iterations carry no per-element selects).
@@ -664,8 +681,7 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(
         // The DMA into a buffer is issued only after this wave's own reads of it (iteration j - 1)
         // have returned, which their use by the MFMAs guarantees.
         constexpr int kDmaOps = 2 * (QT / 8 / 64) + 2;  // vector-memory instructions per issue()
-        if (nmine > 0) issue(wave, qA, oA, lA);
-        for (int j = 0; j < nmine; j += 2) {
+        for (int j = 0; j < nmine; j += 2) {  // iteration `wave` is already in flight into buffer A
             const int itn = wave + NW * j;
             if (j + 1 < nmine) {
                 issue(itn + NW, qB, oB, lB);
@@ -684,53 +700,58 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(
             run(itn + NW, qB, oB, lB);
         }
 
-        // Sum the 4 waves' partial dK^T / dV^T (lane = key, element i = column
-        // 32dt + (i/4)*8 + 4hh + i%4) through LDS: [64 keys][HD] fp32 per (tensor, wave), 16-byte
-        // chunks XOR-swizzled by row.
+        // Every wave is done with its tiles and its DMA: the tile space is free.
         __syncthreads();
+        if (ui + 1 < nunits) {  // the next unit's K / V and first tiles (into the A buffers), in flight during
+            const int un = nkb - 1 - pj;  // the reduction, which uses only the B buffers
+            load_kv(un * BNK);
+            if (wave < group * (nqt - un)) issue_it(wave, un, nqt - un, qA, oA, lA);
+        }
+        // Sum the 4 waves' partial dK^T, then dV^T (lane = key, element i = column
+        // 32dt + (i/4)*8 + 4hh + i%4) through LDS in the B buffers, which the next unit's first tiles
+        // leave alone: [64 keys][HD] fp32 per wave, 16-byte chunks XOR-swizzled by row.
         // The epilogue's addressing is derived from a copy of tid the compiler cannot see through,
         // so it is computed here rather than hoisted to the kernel entry and spilled across the loop.
         int etid;
         __asm__ volatile("v_mov_b32 %0, %1" : "=v"(etid) : "v"(tid));
-        float* stage = reinterpret_cast<float*>(wave < 2 ? (wave == 0 ? qA : oA) : (wave == 2 ? qB : oB));
-        float* sk = stage;
-        float* sv = stage + BNK * HD;
+        float* const st0 = reinterpret_cast<float*>(qB);  // waves 0, 1 stage in qB, waves 2, 3 in oB
+        auto reduce_store = [&](const f32x16 (&acc)[NSL][ND], float mul, u16* out) {
+            float* mine = (wave < 2 ? st0 : reinterpret_cast<float*>(oB)) + (wave & 1) * BNK * HD;
 #pragma unroll
-        for (int sl = 0; sl < NSL; ++sl) {
-            const int kr = 32 * sl + l32;
+            for (int sl = 0; sl < NSL; ++sl) {
+                const int kr = 32 * sl + l32;
 #pragma unroll
-            for (int dt = 0; dt < ND; ++dt)
+                for (int dt = 0; dt < ND; ++dt)
 #pragma unroll
-                for (int g = 0; g < 4; ++g) {
-                    const int cc = ((8 * dt + 2 * g + hh) ^ kr) & (CH4 - 1);
-                    *reinterpret_cast<f32x4*>(sk + kr * HD + 4 * cc) =
-                        f32x4{dk[sl][dt][4 * g], dk[sl][dt][4 * g + 1], dk[sl][dt][4 * g + 2], dk[sl][dt][4 * g + 3]};
-                    *reinterpret_cast<f32x4*>(sv + kr * HD + 4 * cc) =
-                        f32x4{dv[sl][dt][4 * g], dv[sl][dt][4 * g + 1], dv[sl][dt][4 * g + 2], dv[sl][dt][4 * g + 3]};
-                }
-        }
-        __syncthreads();
-        const float* st0 = reinterpret_cast<const float*>(qA);
-        const float* st1 = reinterpret_cast<const float*>(oA);
-        const float* st2 = reinterpret_cast<const float*>(qB);
-        const float* st3 = reinterpret_cast<const float*>(oB);
-#pragma unroll
-        for (int k = 0; k < 2 * BNK * CH4 / 256; ++k) {
-            const int it = etid + 256 * k;
-            const int which = it / (BNK * CH4), rem = it - which * (BNK * CH4);
-            const int row = rem / CH4, c = rem - row * CH4;
-            const int off = which * BNK * HD + row * HD + 4 * ((c ^ row) & (CH4 - 1));
-            f32x4 acc = *reinterpret_cast<const f32x4*>(st0 + off);
-            acc += *reinterpret_cast<const f32x4*>(st1 + off);
-            acc += *reinterpret_cast<const f32x4*>(st2 + off);
-            acc += *reinterpret_cast<const f32x4*>(st3 + off);
-            if (which == 0) acc *= scale;
-            if (kb0 + row < T) {
-                u16* dst = (which == 0 ? dK : dV) + kvoff + (size_t)(kb0 + row) * lk.st + 4 * c;
-                *reinterpret_cast<u32x2*>(dst) = u32x2{E::pack2(acc[0], acc[1]), E::pack2(acc[2], acc[3])};
+                    for (int g = 0; g < 4; ++g) {
+                        const int cc = ((8 * dt + 2 * g + hh) ^ kr) & (CH4 - 1);
+                        *reinterpret_cast<f32x4*>(mine + kr * HD + 4 * cc) =
+                            f32x4{acc[sl][dt][4 * g], acc[sl][dt][4 * g + 1], acc[sl][dt][4 * g + 2], acc[sl][dt][4 * g + 3]};
+                    }
             }
-        }
-        __syncthreads();  // the staging area is the next unit's tile space
+            // LDS-only barriers: the loads and DMA of the next unit (K / V registers, A buffers) stay in
+            // flight; its loop waits for them (vmcnt) before reading either.
+            barrier_lds();
+#pragma unroll
+            for (int k = 0; k < BNK * CH4 / 256; ++k) {
+                const int it = etid + 256 * k;
+                const int row = it / CH4, c = it - row * CH4;
+                const int off = row * HD + 4 * ((c ^ row) & (CH4 - 1));
+                const float* s2 = reinterpret_cast<const float*>(oB);
+                f32x4 sum = *reinterpret_cast<const f32x4*>(st0 + off);
+                sum += *reinterpret_cast<const f32x4*>(st0 + BNK * HD + off);
+                sum += *reinterpret_cast<const f32x4*>(s2 + off);
+                sum += *reinterpret_cast<const f32x4*>(s2 + BNK * HD + off);
+                sum *= mul;
+                if (kb0 + row < T) {
+                    u16* dst = out + kvoff + (size_t)(kb0 + row) * lk.st + 4 * c;
+                    *reinterpret_cast<u32x2*>(dst) = u32x2{E::pack2(sum[0], sum[1]), E::pack2(sum[2], sum[3])};
+                }
+            }
+            barrier_lds();  // the staging area is free again (for dV, then for the next unit's B tiles)
+        };
+        reduce_store(dk, scale, dK);
+        reduce_store(dv, 1.f, dV);
     }
 }
 
