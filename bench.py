@@ -4,7 +4,8 @@
 
 A step is one forward + backward of the hot path through the drop-in C ABI (nn_fa_fwd then nn_fa_bwd,
 include/nanonemo_fa.h) on synthetic N(0,1) inputs already resident in HBM, with outputs and the backward
-workspace allocated once. Default workload: B=8, T=1024, 12 query / 4 KV heads, head_dim 64, bf16 (the
+workspace allocated once. The same step captured once into a HIP graph and replayed K times is reported as
+graph_ms_per_step (the reference benchmark's method, without its cache flush). Default workload: B=8, T=1024, 12 query / 4 KV heads, head_dim 64, bf16 (the
 north-star shape of BASELINE.json). W untimed steps, then K timed steps between device
 synchronisations. The same pair through the torch.library ops (nanonemo::flash_attn +
 nanonemo::flash_attn_bwd, which add output allocation and Python dispatch) is timed beside it as
@@ -201,11 +202,14 @@ def main():
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
     ptr = {n: t.data_ptr() for n, t in dict(q=q, k=k, v=v, do=do, o=o, lse=lse, dq=dq, dk=dk, dv=dv, ws=ws).items()}
 
-    def step_abi():
-        """One fwd+bwd through the C ABI (the drop-in boundary) with outputs already allocated."""
-        check(L.nn_fa_fwd(ptr["q"], ptr["k"], ptr["v"], ptr["o"], ptr["lse"], B, H, KVH, T, D, dt_code, scale, sp))
+    def step_abi_on(st):
+        """One fwd+bwd through the C ABI (the drop-in boundary) on stream st, outputs already allocated."""
+        check(L.nn_fa_fwd(ptr["q"], ptr["k"], ptr["v"], ptr["o"], ptr["lse"], B, H, KVH, T, D, dt_code, scale, st))
         check(L.nn_fa_bwd(ptr["do"], ptr["q"], ptr["k"], ptr["v"], ptr["o"], ptr["lse"], ptr["dq"], ptr["dk"],
-                          ptr["dv"], ptr["ws"], ws_bytes, B, H, KVH, T, D, dt_code, scale, sp))
+                          ptr["dv"], ptr["ws"], ws_bytes, B, H, KVH, T, D, dt_code, scale, st))
+
+    def step_abi():
+        step_abi_on(sp)
 
     def step_op():
         """The same pair through the torch.library ops (allocates outputs with the caching allocator)."""
@@ -235,6 +239,19 @@ def main():
     # The headline: K steps through the C ABI, bracketed by device synchronisations.
     ms = timed(step_abi, args.steps)
     op_ms = timed(step_op, args.steps)
+    # The same C-ABI step captured once into a HIP graph and replayed (no host launch cost per kernel).
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(stream)
+    with torch.cuda.stream(side):
+        step_abi_on(side.cuda_stream)
+    stream.wait_stream(side)
+    torch.cuda.synchronize()
+    with torch.cuda.graph(graph):
+        step_abi_on(torch.cuda.current_stream().cuda_stream)
+    for _ in range(args.warmup):
+        graph.replay()
+    graph_ms = timed(graph.replay, args.steps)
     if args.profile_only:
         # The standalone preprocessing pass (nn_fa_bwd runs it fused into the dQ kernel), so that its
         # HBM traffic and rate have rocprofv3 records of their own.
@@ -408,6 +425,7 @@ def main():
         },
         "pct_of_bf16_peak": round(100 * value / PEAK_TFLOPS, 2),
         "op_ms_per_step": round(op_ms, 5),
+        "graph_ms_per_step": round(graph_ms, 5),
         "rope_qk": {
             "kernel_us": round(rope_us, 2),
             "GBps": round(rope_bytes / (rope_us * 1e-6) / 1e9, 1),
