@@ -66,9 +66,11 @@ constexpr int kF16 = 0;
 constexpr int kBF16 = 1;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
-// The forward keeps a stale running max until a row's max grows by more than this (base-2
-// units): p = exp2(s - m) then stays <= 2^8, far inside fp32 and the 16-bit formats.
-constexpr float kRescaleLog2 = 8.0f;
+// The forward keeps a stale running max m until a row's exponentials exp2(s - m) grow past this
+// bound (base-2 units): p <= 2^24 stays exact in the exponent range of fp32 and the 16-bit formats, and
+// a row's 16 values of a sub-tile then sum to at most 2^28.
+constexpr float kGrowLog2 = 24.0f;
+constexpr float kPsumMax = 16.0f * 16777216.0f;  // 16 * 2^kGrowLog2
 
 #define LDS_AS(T, p) ((__attribute__((address_space(3))) T*)(p))
 
@@ -291,6 +293,7 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_kernel(const u16* __restrict__ 
 #pragma unroll
     for (int dt = 0; dt < ND; ++dt) oacc[dt] = f32x16{};
     float mb = -INFINITY, lsum = 0.f;
+    bool first = true;  // wave-uniform: no sub-tile processed yet
 
     // Per-lane LDS offsets: K row operand (key l32 + 32t, columns 16ks + 8hh; add 32t*HD) and
     // V^T column operand (keys 16c + 8x + 4hh.., column 32dt + l32; add 16c*HD).
@@ -312,9 +315,10 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_kernel(const u16* __restrict__ 
     //   * K operands of sub-tile t+2 are read from LDS while sub-tile t is processed, so the S^T
     //     MFMAs of sub-tile t+1, issued at the top of step t, never wait on LDS;
     //   * the V^T operands of step t are read before its exponentials;
-    //   * the running max is updated without branching (a stale max is kept unless a row grows by
-    //     more than 2^8); the rescale of the row sum and O, and its exponential, sit in a rare
-    //     branch placed just before the P V MFMAs.
+    //   * no max is taken per sub-tile: p = exp2(s * sl2 - mb) against the stale running max mb,
+    //     and the row sums of p, which P V needs anyway, show when a row has outgrown mb. Then (rare:
+    //     a row's first sub-tile, where mb = -inf, and large jumps of its max) the wave takes the
+    //     true max, rescales the row sum and O, and recomputes p, just before the P V MFMAs.
     // MASK: the tile crosses the diagonal or T.
     auto tile = [&](auto mask_tag, int k0, const u16* kb, const u16* vb) {
         constexpr bool MASK = decltype(mask_tag)::value;
@@ -354,37 +358,48 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_kernel(const u16* __restrict__ 
 #pragma unroll
                 for (int i = 0; i < 16; ++i) cur[i] = (32 * t + (i >> 2) * 8 + (i & 3) > lim) ? -INFINITY : cur[i];
             }
-            float mx = cur[0];
-#pragma unroll
-            for (int i = 1; i < 16; ++i) mx = fmaxf(mx, cur[i]);
-            mx = pair_max(mx);
-            // mb is the running max in base-2 units; it moves only when the row grows by more than
-            // 2^kRescaleLog2 (always on the first sub-tile, where mb = -inf).
-            const float mxb = mx * sl2;
-            const bool grow = mxb - mb > kRescaleLog2;
-            const float mold = mb;
-            mb = grow ? mxb : mb;
-#pragma unroll
-            for (int i = 0; i < 16; ++i) cur[i] = fast_exp2(fmaf(cur[i], sl2, -mb));
+            // p against the stale max; a lane's 16 values sum to psum (of the 16-bit p that P V uses).
+            f32x16 pv;
             u16x8 pf[2];
             float psum = 0.f;
+            auto exps = [&]() {
 #pragma unroll
-            for (int half = 0; half < 2; ++half) {
-                pf[half] = pack8<DT>(cur, 8 * half);  // P^T chunk 2t+half: keys 16(2t+half) + (j/4)*8 + 4hh + j%4
-                const u32x4 pw = __builtin_bit_cast(u32x4, pf[half]);
-                psum = E::add_pair(pw[0], psum);
-                psum = E::add_pair(pw[1], psum);
-                psum = E::add_pair(pw[2], psum);
-                psum = E::add_pair(pw[3], psum);
-            }
-            // Rare: some row's max moved, so its sum and O are rescaled by 2^(old - new) (0 on the
-            // first sub-tile, 1 for rows that kept theirs). psum >= 0 always holds; testing it keeps
-            // the branch after the exponentials, in one scheduling region with the next S^T MFMAs.
-            if (__builtin_amdgcn_ballot_w64(grow && psum >= 0.f)) {
-                const float corr = fast_exp2(mold - mb);
+                for (int i = 0; i < 16; ++i) pv[i] = fast_exp2(fmaf(cur[i], sl2, -mb));
+                psum = 0.f;
+#pragma unroll
+                for (int half = 0; half < 2; ++half) {
+                    pf[half] = pack8<DT>(pv, 8 * half);  // P^T chunk 2t+half: keys 16(2t+half) + (j/4)*8 + 4hh + j%4
+                    const u32x4 pw = __builtin_bit_cast(u32x4, pf[half]);
+                    psum = E::add_pair(pw[0], psum);
+                    psum = E::add_pair(pw[1], psum);
+                    psum = E::add_pair(pw[2], psum);
+                    psum = E::add_pair(pw[3], psum);
+                }
+            };
+            // The row's true max sets the new mb (both half-waves agree through pair_max); the row sum
+            // and O are rescaled by 2^(old - new), and p is (re)computed.
+            auto rescale = [&]() {
+                float mx = cur[0];
+#pragma unroll
+                for (int i = 1; i < 16; ++i) mx = fmaxf(mx, cur[i]);
+                mx = pair_max(mx);
+                const float mnew = fmaxf(mb, mx * sl2);
+                const float corr = fast_exp2(mb - mnew);
+                mb = mnew;
                 lsum *= corr;
 #pragma unroll
                 for (int dt = 0; dt < ND; ++dt) oacc[dt] *= corr;
+                exps();
+            };
+            if (first) {
+                // This wave's first sub-tile (keys 0..31, which hold key 0 for every row, so every
+                // row's max is finite): mb = -inf until here, so the max is taken directly.
+                rescale();
+                first = false;
+            } else {
+                exps();
+                // Rare: some row outgrew mb (its psum past the bound, or inf).
+                if (__builtin_amdgcn_ballot_w64(psum > kPsumMax)) rescale();
             }
             lsum += psum;
 #pragma unroll
