@@ -182,28 +182,58 @@ __device__ inline DmaLane dma_lane(int lane) {
     return {(uint32_t)rl, (uint32_t)swz_chunk<W>(rl, cl) * 16, (uint32_t)swz_chunk<W>(rl + 8, cl) * 16};
 }
 
-// Copies rows [r0, r0 + ROWS) of a [T][W] global matrix with row stride `ld` elements (rows past
-// T - 1 repeat row T - 1; their results are masked by the callers) into a swizzled row-major LDS
-// tile, 16 bytes per lane. `g`, `ld`, `r0`, `T`, `lds` and `wave` are wave-uniform: each copy
-// instruction addresses a uniform tile base plus a 32-bit per-lane byte offset, and its LDS
-// destination is the uniform base + 16 * lane. The per-lane terms are re-derived from `dl` at
-// each call rather than kept per instruction across the caller's loop.
+// Per-lane byte offsets of the copy instructions (this wave's share) of a [ROWS][W] tile with row
+// stride `ld` elements, relative to the tile's first row: computed once per kernel, so that a copy
+// of a tile that does not reach past row T - 1 costs no per-lane address arithmetic.
 template <int W, int ROWS, int NW>
-__device__ inline void dma_rows(const u16* __restrict__ g, int ld, int r0, int T, u16* lds, int wave, DmaLane dl) {
+struct DmaOffs {
+    static constexpr int N = ROWS * (W / 8) / (64 * NW);
+    uint32_t o[N];
+};
+template <int W, int ROWS, int NW>
+__device__ inline DmaOffs<W, ROWS, NW> dma_offsets(int lane, int wave, int ld) {
+    constexpr int CH = W / 8;
+    const DmaLane dl = dma_lane<W>(lane);
+    DmaOffs<W, ROWS, NW> r;
+#pragma unroll
+    for (int it = 0; it < DmaOffs<W, ROWS, NW>::N; ++it) {
+        const int k = it * NW + wave;  // copy instruction index within the tile
+        r.o[it] = (dl.rl + (uint32_t)(k * (64 / CH))) * (uint32_t)ld * 2 + ((W == 64 && (k & 1)) ? dl.cB1 : dl.cB0);
+    }
+    return r;
+}
+
+// Buffer resource word 3 for raw (unswizzled, stride 0) buffer access on gfx9-family parts.
+constexpr int kBufWord3 = 0x00020000;
+
+// Copies rows [r0, r0 + ROWS) of a [T][W] global matrix with row stride `ld` elements into a
+// swizzled row-major LDS tile, 16 bytes per lane. `g`, `ld`, `r0`, `T`, `lds` and `wave` are
+// wave-uniform, and `fo` holds this lane's offsets for stride `ld` (dma_offsets). The copies are
+// buffer loads: the tile's base and extent live in a scalar buffer descriptor and each lane adds its
+// 32-bit offset, so they cost no per-lane address arithmetic. The descriptor's extent ends at row
+// T - 1, so rows past it read as zeros (their results are masked by the callers). The LDS
+// destination of a copy is the uniform base + 16 * lane.
+template <int W, int ROWS, int NW>
+__device__ inline void dma_rows(const u16* __restrict__ g, int ld, int r0, int T, u16* lds, int wave,
+                                const DmaOffs<W, ROWS, NW>& fo) {
     constexpr int CH = W / 8, NCH = ROWS * CH;
     static_assert(NCH % (64 * NW) == 0 && 64 % CH == 0, "tile must split evenly over the block's waves");
-    __asm__ volatile("" : "+v"(dl.rl), "+v"(dl.cB0), "+v"(dl.cB1));
-    const char* gt = reinterpret_cast<const char*>(g + (size_t)r0 * ld);
-    const uint32_t ldB = (uint32_t)ld * 2;
-    const uint32_t limB = (uint32_t)min(T - 1 - r0, ROWS - 1) * ldB;
+#if defined(__HIP_DEVICE_COMPILE__)  // the buffer descriptor type exists in the device pass only
+    const int wu = __builtin_amdgcn_readfirstlane(wave);
+    // readfirstlane yields an int: each half goes through uint32_t before widening, or a low word with
+    // bit 31 set would sign-extend into the high word.
+    const uint64_t ga = reinterpret_cast<uint64_t>(g + (size_t)r0 * ld);
+    const uint32_t ghi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(ga >> 32));
+    const uint32_t glo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)ga);
+    void* gt = reinterpret_cast<void*>(((uint64_t)ghi << 32) | glo);
+    const int nbytes = __builtin_amdgcn_readfirstlane(min(T - r0, ROWS) * ld * 2);
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(gt, 0, nbytes, kBufWord3);
 #pragma unroll
     for (int it = 0; it < NCH / (64 * NW); ++it) {
-        const int k = it * NW + wave;  // copy instruction index within the tile
-        const uint32_t rb = (dl.rl + (uint32_t)(k * (64 / CH))) * ldB;
-        const uint32_t cb = (W == 64 && (k & 1)) ? dl.cB1 : dl.cB0;
-        __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(gt + (min(rb, limB) + cb)),
-                                         LDS_AS(void, lds + k * 64 * 8), 16, 0, 0);
+        const int k = it * NW + wu;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, LDS_AS(void, lds + k * 64 * 8), 16, fo.o[it], 0, 0, 0);
     }
+#endif
 }
 
 // Element strides of a [B][heads][T][D] tensor view whose D stride is 1: batch, head and row
@@ -281,7 +311,7 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_kernel(const u16* __restrict__ 
 
     const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const DmaLane dl = dma_lane<HD>(lane);
+    const DmaOffs<HD, BN, NW> dfo = dma_offsets<HD, BN, NW>(lane, wave, lk.st);
     const int g16 = (lane >> 4) & 1;  // which 16-column half of a 32-wide MFMA tile this lane reads
     const int q0 = qb * BM, qw = q0 + wave * 32, qrow = qw + l32;
 
@@ -307,8 +337,8 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_kernel(const u16* __restrict__ 
 
     const int ntiles = (min(q0 + BM, T) + BN - 1) / BN;
     auto issue = [&](int it, u16* kb, u16* vb) {
-        dma_rows<HD, BN, NW>(Kp, lk.st, it * BN, T, kb, wave, dl);
-        dma_rows<HD, BN, NW>(Vp, lk.st, it * BN, T, vb, wave, dl);
+        dma_rows<HD, BN, NW>(Kp, lk.st, it * BN, T, kb, wave, dfo);
+        dma_rows<HD, BN, NW>(Vp, lk.st, it * BN, T, vb, wave, dfo);
     };
     // One 128-key tile as four 32-key sub-tiles, software-pipelined so that the matrix unit and the
     // VALU have independent work in the same stretch of straight-line code:
@@ -521,7 +551,7 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(
     const int b = bk / KVH, kvh = bk - b * KVH, group = H / KVH;
     const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
     const int wave = tid >> 6;  // a uniform copy in an SGPR costs this kernel more than it saves
-    const DmaLane dl = dma_lane<HD>(lane);
+    const DmaOffs<HD, BM, 1> dfo = dma_offsets<HD, BM, 1>(lane, 0, lq.st);
     const int g16 = (lane >> 4) & 1;
     const size_t kvoff = lk.at(b, kvh);
 
@@ -557,8 +587,8 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(
         const size_t ro = ((size_t)b * H + hq) * T;  // first row of the head's [T] vectors
         const size_t qo = lq.at(b, hq);
         const int q0 = (qtf + itu % nqq) * BM;
-        dma_rows<HD, BM, 1>(Q + qo, lq.st, q0, T, qs + wu * QT, 0, dl);
-        dma_rows<HD, BM, 1>(dO + qo, lq.st, q0, T, os + wu * QT, 0, dl);
+        dma_rows<HD, BM, 1>(Q + qo, lq.st, q0, T, qs + wu * QT, 0, dfo);
+        dma_rows<HD, BM, 1>(dO + qo, lq.st, q0, T, os + wu * QT, 0, dfo);
         const uint32_t lo = (uint32_t)min(lane, T - 1 - q0) * 4;  // rows past T repeat row T - 1
         __builtin_amdgcn_global_load_lds(reinterpret_cast<const char*>(nLvec + ro + q0) + lo, LDS_AS(void, ls + wu * 2 * BM), 4, 0, 0);
         __builtin_amdgcn_global_load_lds(reinterpret_cast<const char*>(nDvec + ro + q0) + lo, LDS_AS(void, ls + wu * 2 * BM + BM), 4, 0, 0);
@@ -809,7 +839,7 @@ __global__ __launch_bounds__(256, 2) void fa_bwd_dq_kernel(const u16* __restrict
 
     const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const DmaLane dl = dma_lane<HD>(lane);
+    const DmaOffs<HD, BN, NW> dfo = dma_offsets<HD, BN, NW>(lane, wave, lk.st);
     const int g16 = (lane >> 4) & 1;
     const int q0 = qb * BM, qw = q0 + wave * 32, qrow = qw + l32;
     const int qc_ = min(qrow, T - 1);
@@ -849,8 +879,8 @@ __global__ __launch_bounds__(256, 2) void fa_bwd_dq_kernel(const u16* __restrict
 
     const int ntiles = (min(q0 + BM, T) + BN - 1) / BN;
     auto issue = [&](int it, u16* kb, u16* vb) {
-        dma_rows<HD, BN, NW>(Kp, lk.st, it * BN, T, kb, wave, dl);
-        dma_rows<HD, BN, NW>(Vp, lk.st, it * BN, T, vb, wave, dl);
+        dma_rows<HD, BN, NW>(Kp, lk.st, it * BN, T, kb, wave, dfo);
+        dma_rows<HD, BN, NW>(Vp, lk.st, it * BN, T, vb, wave, dfo);
     };
     // -D enters as the initial value of every dP^T accumulator (the same for all of a lane's keys).
     f32x16 ndv;
