@@ -654,8 +654,16 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(
         // step's operands are read from LDS while the first step's products run.
         // MASK: the iteration crosses the diagonal or T (a separate instantiation, so that unmasked
         // iterations carry no per-element selects).
-        auto compute = [&](auto mask_tag, int qbase, const u16* qs, const u16* os, const float* ls) {
+        // DMA: the next iteration's tiles (iteration nitn into nqs / nos / nls) are copied during this
+        // one, their copy instructions spread over the MFMAs (the CU's copy path accepts them only so
+        // fast, and an in-order wave that issued them back to back would stall on it with its MFMA
+        // pipe idle).
+        constexpr int kDmaOps = 2 * (QT / 8 / 64) + 2;  // vector-memory instructions per issue()
+        auto compute = [&](auto mask_tag, auto dma_tag, int qbase, const u16* qs, const u16* os, const float* ls,
+                           int nitn, u16* nqs, u16* nos, float* nls) {
             constexpr bool MASK = decltype(mask_tag)::value;
+            constexpr bool DMA = decltype(dma_tag)::value;
+            if constexpr (DMA) issue(nitn, nqs, nos, nls);
             const u16* qb_ = qs + wave * QT;
             const u16* ob_ = os + wave * QT;
             const float* lb_ = ls + wave * 2 * BM;
@@ -714,35 +722,39 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(
                     }
                 }
             }
+            if constexpr (DMA) {  // three MFMAs, then one copy instruction, kDmaOps times (denser stalls on
+                                  // the copy path, sparser leaves the last copies' latency exposed)
+#pragma unroll
+                for (int k = 0; k < kDmaOps; ++k) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 3, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+                }
+            }
         };
-        auto run = [&](int itn, const u16* qs, const u16* os, const float* ls) {
+        auto run = [&](auto dma_tag, int itn, const u16* qs, const u16* os, const float* ls, int nitn, u16* nqs,
+                       u16* nos, float* nls) {
             const int qbase = qbase_of(itn);
             if ((kb0 + BNK - 1 > qbase) || (qbase + BM > T) || (kb0 + BNK > T))
-                compute(std::true_type{}, qbase, qs, os, ls);
+                compute(std::true_type{}, dma_tag, qbase, qs, os, ls, nitn, nqs, nos, nls);
             else
-                compute(std::false_type{}, qbase, qs, os, ls);
+                compute(std::false_type{}, dma_tag, qbase, qs, os, ls, nitn, nqs, nos, nls);
         };
         // Double-buffered: this wave's iteration j uses buffer j % 2 while j + 1 streams into the other.
         // The DMA into a buffer is issued only after this wave's own reads of it (iteration j - 1)
         // have returned, which their use by the MFMAs guarantees.
-        constexpr int kDmaOps = 2 * (QT / 8 / 64) + 2;  // vector-memory instructions per issue()
         for (int j = 0; j < nmine; j += 2) {  // iteration `wave` is already in flight into buffer A
             const int itn = wave + NW * j;
-            if (j + 1 < nmine) {
-                issue(itn + NW, qB, oB, lB);
-                wait_vmem_keep<kDmaOps>();
-            } else {
-                wait_vmem();
-            }
-            run(itn, qA, oA, lA);
+            wait_vmem();  // this iteration's tiles, copied during the previous one
+            if (j + 1 < nmine)
+                run(std::true_type{}, itn, qA, oA, lA, itn + NW, qB, oB, lB);
+            else
+                run(std::false_type{}, itn, qA, oA, lA, 0, qB, oB, lB);
             if (j + 1 >= nmine) break;
-            if (j + 2 < nmine) {
-                issue(itn + 2 * NW, qA, oA, lA);
-                wait_vmem_keep<kDmaOps>();
-            } else {
-                wait_vmem();
-            }
-            run(itn + NW, qB, oB, lB);
+            wait_vmem();
+            if (j + 2 < nmine)
+                run(std::true_type{}, itn + NW, qB, oB, lB, itn + 2 * NW, qA, oA, lA);
+            else
+                run(std::false_type{}, itn + NW, qB, oB, lB, 0, qA, oA, lA);
         }
 
         // Every wave is done with its tiles and its DMA: the tile space is free.
