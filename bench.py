@@ -1,6 +1,7 @@
 """Benchmark of the causal GQA FlashAttention-2 forward + backward on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--dtype bf16|fp16] [--batch 8] [--seq 1024]
+    python bench.py --sweep        # step and per-kernel times over the SWEEP shapes, one JSON line each
 
 A step is one forward + backward of the hot path through the drop-in C ABI (nn_fa_fwd then nn_fa_bwd,
 include/nanonemo_fa.h) on synthetic N(0,1) inputs already resident in HBM, with outputs and the backward
@@ -109,7 +110,97 @@ def parse():
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="budget of the CPU baseline sample")
     p.add_argument("--profile-only", action="store_true", help="only the timed steps (for rocprofv3)")
     p.add_argument("--prewarm", type=float, default=1.0, help="seconds of untimed steps after the warmup")
+    p.add_argument("--sweep", action="store_true",
+                   help="instead of the headline line: one JSON line per shape of SWEEP (step and per-kernel times)")
     return p.parse_args()
+
+
+# --sweep shapes: (label, B, T, H, KVH, D, dtype, input scale). The BASELINE.json configurations 2-4 first
+# (config 2 in its fp16 and the headline's bf16), then other head dims, GQA ratios and lengths.
+SWEEP = [
+    ("config 2 (fp16)", 8, 1024, 12, 4, 64, "fp16", 1.0),
+    ("config 2 (bf16, the headline)", 8, 1024, 12, 4, 64, "bf16", 1.0),
+    ("config 3", 32, 1024, 12, 4, 64, "bf16", 3.0),
+    ("config 4", 2, 8192, 12, 4, 64, "bf16", 1.0),
+    ("config 1 shape", 1, 256, 12, 4, 64, "bf16", 1.0),
+    ("head_dim 32", 8, 1024, 12, 4, 32, "bf16", 1.0),
+    ("MHA (12 KV heads)", 8, 1024, 12, 12, 64, "bf16", 1.0),
+    ("MQA (1 KV head)", 8, 1024, 12, 1, 64, "bf16", 1.0),
+    ("T=2048", 4, 2048, 12, 4, 64, "bf16", 1.0),
+    ("T=4096", 2, 4096, 12, 4, 64, "bf16", 1.0),
+    ("T=16384", 1, 16384, 12, 4, 64, "bf16", 1.0),
+]
+
+
+def sweep(args):
+    """Per shape: the fwd+bwd step through the C ABI and each kernel alone, HIP events on the launch
+    stream, after warm-up and about 0.3 s of settling steps. One JSON line per shape."""
+    import torch
+
+    from nanonemo_amd.kernels.hip import DTYPE_BF16, DTYPE_F16, check, lib
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    L = lib()
+    stream = torch.cuda.current_stream()
+    sp = stream.cuda_stream
+    for label, B, T, H, KVH, D, dts, mult in SWEEP:
+        dtype = torch.bfloat16 if dts == "bf16" else torch.float16
+        code = DTYPE_BF16 if dts == "bf16" else DTYPE_F16
+        scale = 1.0 / math.sqrt(D)
+        torch.manual_seed(0)
+        q, do = ((torch.randn(B, H, T, D, device=dev) * mult).to(dtype) for _ in range(2))
+        k, v = ((torch.randn(B, KVH, T, D, device=dev) * mult).to(dtype) for _ in range(2))
+        o, dq = torch.empty_like(q), torch.empty_like(q)
+        dk, dv = torch.empty_like(k), torch.empty_like(v)
+        lse = torch.empty(B, H, T, dtype=torch.float32, device=dev)
+        wsb = L.nn_fa_bwd_workspace_size(B, H, KVH, T, D)
+        ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
+        a = (B, H, KVH, T, D, code, scale, sp)
+        fwd = lambda: L.nn_fa_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(), *a)  # noqa: E731
+        bwd = lambda: L.nn_fa_bwd(do.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),  # noqa: E731
+                                  lse.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), ws.data_ptr(), wsb, *a)
+        dqk = lambda: L.nn_fa_bwd_dq(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), do.data_ptr(),  # noqa: E731
+                                     lse.data_ptr(), ws.data_ptr(), wsb, dq.data_ptr(), *a)
+        dkdv = lambda: L.nn_fa_bwd_dkdv(q.data_ptr(), k.data_ptr(), v.data_ptr(), do.data_ptr(), ws.data_ptr(),  # noqa: E731
+                                        wsb, dk.data_ptr(), dv.data_ptr(), *a)
+
+        def step():
+            check(fwd())
+            check(bwd())
+
+        for _ in range(max(args.warmup, 3)):
+            step()
+        t_end = time.perf_counter() + 0.3
+        while time.perf_counter() < t_end:
+            for _ in range(20):
+                step()
+            torch.cuda.synchronize()
+
+        def events(fn, reps):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            for _ in range(reps):
+                fn()
+            e1.record(stream)
+            e1.synchronize()
+            return e0.elapsed_time(e1) * 1e3 / reps
+
+        pairs = B * H * T * (T + 1) / 2
+        reps = max(5, min(args.steps, int(30000 / events(step, 3))))  # about 30 ms of each measurement
+        step_us = events(step, reps)
+        us = {n: events(lambda fn=fn: check(fn()), reps) for n, fn in (("fwd", fwd), ("dq", dqk), ("dkdv", dkdv))}
+        tf = lambda flop, t: round(flop / t / 1e6, 1)  # noqa: E731
+        print(json.dumps({
+            "shape": label, "B": B, "T": T, "H": H, "KVH": KVH, "D": D, "dtype": dts, "input_scale": mult,
+            "step_us": round(step_us, 2), "tflops": tf(12 * D * pairs, step_us),
+            "pct_of_peak": round(100 * 12 * D * pairs / step_us / 1e6 / PEAK_TFLOPS, 2),
+            "fwd_us": round(us["fwd"], 2), "fwd_tflops": tf(4 * D * pairs, us["fwd"]),
+            "dq_us": round(us["dq"], 2), "dq_tflops": tf(2 * D * pairs, us["dq"]),
+            "dkdv_us": round(us["dkdv"], 2), "dkdv_tflops": tf(6 * D * pairs, us["dkdv"]),
+        }), flush=True)
+        del q, k, v, do, o, dq, dk, dv, lse, ws
+        torch.cuda.empty_cache()
 
 
 def cpu_baseline(B, H, KVH, T, D, budget_s):
@@ -163,6 +254,9 @@ def cpu_baseline(B, H, KVH, T, D, budget_s):
 
 def main():
     args = parse()
+    if args.sweep and args.gpus == 1:
+        sweep(args)
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(
             "bench.py measures one GPU only: this build's hot path (causal GQA attention) runs per GPU on its "

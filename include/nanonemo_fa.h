@@ -50,7 +50,9 @@ int nn_fa_fwd_strided(const void* q, const void* k, const void* v, void* o, floa
                       int dtype, float scale, void* stream);
 
 /* Bytes of device workspace the backward needs: -rowsum(dO * o) and -lse / scale, one fp32 each
- * per query row. The caller allocates it, 256-byte aligned; its contents on entry
+ * per query row, and, for shapes whose B * KVH * ceil(T / 128) dK/dV work units are too few to fill
+ * the chip (under 256), split partials of dk and dv: S * 2 * B * KVH * T * D fp32 with
+ * S = min(16, ceil(256 / units)). The caller allocates it, 256-byte aligned; its contents on entry
  * do not matter. */
 size_t nn_fa_bwd_workspace_size(int64_t B, int64_t H, int64_t KVH, int64_t T, int64_t D);
 
@@ -86,10 +88,12 @@ int nn_fa_bwd_pre(const void* o, const void* dO, const float* lse, void* workspa
                   void* stream);
 
 /* Backward, dk and dv (keys outer; recomputes P from the workspace's -lse/scale and uses its -D).
- * Needs the workspace prepared by nn_fa_bwd_dq or nn_fa_bwd_pre. Together with nn_fa_bwd_dq it
- * replaces bwd_kernel<HD>, flash_attn.cu:176-340 with its launch at :393-401 and the casts at :404. */
+ * Needs the workspace prepared by nn_fa_bwd_dq or nn_fa_bwd_pre. When the shape splits the dK/dV
+ * work (see nn_fa_bwd_workspace_size), it writes the split partials into the workspace and sums them
+ * in a fixed order (deterministic). Together with nn_fa_bwd_dq it replaces bwd_kernel<HD>,
+ * flash_attn.cu:176-340 with its launch at :393-401 and the casts at :404. */
 int nn_fa_bwd_dkdv(const void* q, const void* k, const void* v, const void* dO,
-                   const void* workspace, size_t workspace_bytes, void* dk, void* dv,
+                   void* workspace, size_t workspace_bytes, void* dk, void* dv,
                    int64_t B, int64_t H, int64_t KVH, int64_t T, int64_t D,
                    int dtype, float scale, void* stream);
 

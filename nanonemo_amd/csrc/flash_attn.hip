@@ -40,6 +40,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <algorithm>
 #include <string>
 #include <type_traits>
 
@@ -519,7 +520,10 @@ __global__ __launch_bounds__(256) void fa_bwd_pre_kernel(const u16* __restrict__
 // both 32-key slabs. The GQA sum over the H/KVH query heads of a KV head happens in the
 // accumulators. At the end of a unit the 4 partial dK / dV are summed through LDS and stored once
 // in the output dtype (no atomics, no fp32 round trip through HBM). A block takes unit j and unit
-// nkb-1-j, so every block carries the same causal work. Per 32-query step and 32-key slab:
+// nkb-1-j, so every block carries the same causal work. When those pairs are too few to fill the
+// chip, nsplit > 1 blocks share each pair: block s takes iterations [s n / nsplit, (s+1) n / nsplit)
+// of each unit (n of them) and stores its fp32 partial sums into `part` instead, which
+// fa_bwd_dkdv_sum_kernel adds in split order. Per 32-query step and 32-key slab:
 //   S' = Q K^T - lse/scale, dP' = dO V^T - D   (A = Q / dO rows from LDS, B = K / V registers;
 //                                              the accumulators start from -lse/scale and -D)
 //   P = exp2(S' * sl2), dS = P dP'
@@ -529,7 +533,8 @@ template <int HD, int DT>
 __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(
     const u16* __restrict__ Q, const u16* __restrict__ K, const u16* __restrict__ V, const u16* __restrict__ dO,
     const float* __restrict__ nLvec, const float* __restrict__ nDvec, u16* __restrict__ dK, u16* __restrict__ dV,
-    int BKV, int H, int KVH, int T, int nkb, int nqt, float sl2, float scale, Lay lq, Lay lk) {
+    int BKV, int H, int KVH, int T, int nkb, int nqt, float sl2, float scale, Lay lq, Lay lk, int nsplit,
+    float* __restrict__ part) {
     using E = Elem<DT>;
     constexpr int BNK = 64, BM = 64, NW = 4, NSL = BNK / 32;
     constexpr int NS = HD / 16;
@@ -545,13 +550,18 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(
     __shared__ __attribute__((aligned(16))) float lA[NW * 2 * BM];  // per wave: -lse/scale | -D
     __shared__ __attribute__((aligned(16))) float lB[NW * 2 * BM];
 
-    const int bid = blockIdx.x;
+    const int nbase = BKV * ((nkb + 1) / 2);  // blocks of one split
+    const int sidx = blockIdx.x / nbase;      // this block's split
+    const int bid = blockIdx.x - sidx * nbase;
     const int bk = bid % BKV;
     const int pj = bid / BKV;
     const int b = bk / KVH, kvh = bk - b * KVH, group = H / KVH;
     const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
     const int wave = tid >> 6;  // a uniform copy in an SGPR costs this kernel more than it saves
     const DmaOffs<HD, BM, 1> dfo = dma_offsets<HD, BM, 1>(lane, 0, lq.st);
+    // This split's iterations [first, end) of a unit with n of them.
+    auto first_of = [&](int n) { return (int)((int64_t)sidx * n / nsplit); };
+    auto end_of = [&](int n) { return (int)((int64_t)(sidx + 1) * n / nsplit); };
     const int g16 = (lane >> 4) & 1;
     const size_t kvoff = lk.at(b, kvh);
 
@@ -597,13 +607,17 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(
     // reduction, so that their latency overlaps it.
     const int nunits = nkb - 1 - pj > pj ? 2 : 1;  // an odd unit count leaves the middle unit alone
     load_kv(pj * BNK);
-    if (wave < group * (nqt - pj)) issue_it(wave, pj, nqt - pj, qA, oA, lA);
+    {
+        const int n0 = group * (nqt - pj), i0 = first_of(n0);
+        if (wave < end_of(n0) - i0) issue_it(i0 + wave, pj, nqt - pj, qA, oA, lA);
+    }
 
     for (int ui = 0; ui < nunits; ++ui) {
         const int unit = ui == 0 ? pj : nkb - 1 - pj;
         const int kb0 = unit * BNK;
         const int qt_first = unit, nq = nqt - qt_first, niter = group * nq;
-        const int nmine = wave < niter ? (niter - wave + NW - 1) / NW : 0;  // iterations wave, wave+NW, ...
+        const int ifirst = first_of(niter), nsp = end_of(niter) - ifirst;  // this split's iterations
+        const int nmine = wave < nsp ? (nsp - wave + NW - 1) / NW : 0;  // iterations ifirst + wave + NW j
 
         f32x16 dk[NSL][ND], dv[NSL][ND];
 #pragma unroll
@@ -742,8 +756,8 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(
         // Double-buffered: this wave's iteration j uses buffer j % 2 while j + 1 streams into the other.
         // The DMA into a buffer is issued only after this wave's own reads of it (iteration j - 1)
         // have returned, which their use by the MFMAs guarantees.
-        for (int j = 0; j < nmine; j += 2) {  // iteration `wave` is already in flight into buffer A
-            const int itn = wave + NW * j;
+        for (int j = 0; j < nmine; j += 2) {  // iteration ifirst + wave is already in flight into buffer A
+            const int itn = ifirst + wave + NW * j;
             wait_vmem();  // this iteration's tiles, copied during the previous one
             if (j + 1 < nmine)
                 run(std::true_type{}, itn, qA, oA, lA, itn + NW, qB, oB, lB);
@@ -762,7 +776,8 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(
         if (ui + 1 < nunits) {  // the next unit's K / V and first tiles (into the A buffers), in flight during
             const int un = nkb - 1 - pj;  // the reduction, which uses only the B buffers
             load_kv(un * BNK);
-            if (wave < group * (nqt - un)) issue_it(wave, un, nqt - un, qA, oA, lA);
+            const int n1 = group * (nqt - un), i1 = first_of(n1);
+            if (wave < end_of(n1) - i1) issue_it(i1 + wave, un, nqt - un, qA, oA, lA);
         }
         // Sum the 4 waves' partial dK^T, then dV^T (lane = key, element i = column
         // 32dt + (i/4)*8 + 4hh + i%4) through LDS in the B buffers, which the next unit's first tiles
@@ -772,7 +787,7 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(
         int etid;
         __asm__ volatile("v_mov_b32 %0, %1" : "=v"(etid) : "v"(tid));
         float* const st0 = reinterpret_cast<float*>(qB);  // waves 0, 1 stage in qB, waves 2, 3 in oB
-        auto reduce_store = [&](const f32x16 (&acc)[NSL][ND], float mul, u16* out) {
+        auto reduce_store = [&](const f32x16 (&acc)[NSL][ND], float mul, u16* out, int which) {
             float* mine = (wave < 2 ? st0 : reinterpret_cast<float*>(oB)) + (wave & 1) * BNK * HD;
 #pragma unroll
             for (int sl = 0; sl < NSL; ++sl) {
@@ -801,14 +816,46 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(
                 sum += *reinterpret_cast<const f32x4*>(s2 + BNK * HD + off);
                 sum *= mul;
                 if (kb0 + row < T) {
-                    u16* dst = out + kvoff + (size_t)(kb0 + row) * lk.st + 4 * c;
-                    *reinterpret_cast<u32x2*>(dst) = u32x2{E::pack2(sum[0], sum[1]), E::pack2(sum[2], sum[3])};
+                    if (nsplit == 1) {
+                        u16* dst = out + kvoff + (size_t)(kb0 + row) * lk.st + 4 * c;
+                        *reinterpret_cast<u32x2*>(dst) = u32x2{E::pack2(sum[0], sum[1]), E::pack2(sum[2], sum[3])};
+                    } else {  // this split's partial: part[split][dK | dV][bk][key][HD]
+                        float* dst = part + (((size_t)sidx * 2 + which) * BKV + bk) * T * HD + (size_t)(kb0 + row) * HD + 4 * c;
+                        *reinterpret_cast<f32x4*>(dst) = sum;
+                    }
                 }
             }
             barrier_lds();  // the staging area is free again (for dV, then for the next unit's B tiles)
         };
-        reduce_store(dk, scale, dK);
-        reduce_store(dv, 1.f, dV);
+        reduce_store(dk, scale, dK, 0);
+        reduce_store(dv, 1.f, dV, 1);
+    }
+}
+
+// ------------------------------------------------------------------------------------------
+// Backward, dK / dV with nsplit > 1: dK, dV = the sum over splits s = 0, 1, ... (in that order) of
+// part[s][dK | dV][bk][key][HD] (fp32, dK already scaled), rounded once to the output dtype. One
+// thread per 4 consecutive columns; grid-stride.
+// ------------------------------------------------------------------------------------------
+template <int DT>
+__global__ __launch_bounds__(256) void fa_bwd_dkdv_sum_kernel(const float* __restrict__ part, u16* __restrict__ dK,
+                                                              u16* __restrict__ dV, int nsplit, int BKV, int KVH,
+                                                              int T, int HD, Lay lk) {
+    using E = Elem<DT>;
+    const int64_t per = (int64_t)BKV * T * HD;  // elements of one gradient
+    const int64_t n4 = 2 * per / 4;
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n4; i += (int64_t)gridDim.x * 256) {
+        const int64_t e = 4 * i;
+        const int which = (int)(e / per);
+        const int64_t r = e - which * per;
+        const int bk = (int)(r / ((int64_t)T * HD));
+        const int64_t r2 = r - (int64_t)bk * T * HD;
+        const int key = (int)(r2 / HD), col = (int)(r2 - (int64_t)key * HD);
+        f32x4 acc = *reinterpret_cast<const f32x4*>(part + e);
+        for (int s = 1; s < nsplit; ++s) acc += *reinterpret_cast<const f32x4*>(part + (int64_t)s * 2 * per + e);
+        const int b = bk / KVH, kvh = bk - b * KVH;
+        u16* dst = (which == 0 ? dK : dV) + lk.at(b, kvh) + (size_t)key * lk.st + col;
+        *reinterpret_cast<u32x2*>(dst) = u32x2{E::pack2(acc[0], acc[1]), E::pack2(acc[2], acc[3])};
     }
 }
 
@@ -1014,17 +1061,34 @@ int check_dims(int64_t B, int64_t H, int64_t KVH, int64_t T, int64_t D, int dtyp
 struct Workspace {
     float* nD;
     float* nL;
+    float* part;  // dK / dV split partials (nsplit > 1 only)
+    int nsplit;
     size_t bytes;
 };
 
 size_t round256(size_t n) { return (n + 255) & ~(size_t)255; }
 
-Workspace carve(void* base, int64_t B, int64_t H, int64_t T) {
+// Splits of the dK/dV work: one block per CU (256 on MI355X) is what fills the chip; below that, each
+// block's work is shared by up to 16 blocks whose fp32 partials are summed afterwards, as long as
+// every split keeps at least 8 of the pair's (query head, query tile) iterations (two per wave: a
+// block's fixed cost is about that much work).
+constexpr int64_t kDkdvFill = 256, kDkdvMaxSplit = 16, kDkdvMinIters = 8;
+int dkdv_split(int64_t B, int64_t H, int64_t KVH, int64_t T) {
+    if (B <= 0 || KVH <= 0 || H < KVH || T <= 0) return 1;
+    const int64_t nkb = (T + 63) / 64, base = B * KVH * ((nkb + 1) / 2);
+    if (base >= kDkdvFill) return 1;
+    const int64_t by_fill = (kDkdvFill + base - 1) / base, by_work = (H / KVH) * (nkb + 1) / kDkdvMinIters;
+    return (int)std::max<int64_t>(1, std::min({kDkdvMaxSplit, by_fill, by_work}));
+}
+
+Workspace carve(void* base, int64_t B, int64_t H, int64_t KVH, int64_t T, int64_t D) {
     const size_t vec = round256(4 * (size_t)B * H * T);
     Workspace w;
+    w.nsplit = dkdv_split(B, H, KVH, T);
     w.nD = (float*)base;
     w.nL = (float*)((char*)base + vec);
-    w.bytes = 2 * vec;
+    w.part = w.nsplit > 1 ? (float*)((char*)base + 2 * vec) : nullptr;
+    w.bytes = 2 * vec + (w.nsplit > 1 ? round256((size_t)w.nsplit * 2 * 4 * B * KVH * T * D) : 0);
     return w;
 }
 
@@ -1056,10 +1120,16 @@ int dkdv_impl(const void* q, const void* k, const void* v, const void* dO, const
     const int nqt = nkb;                   // 64-row query tiles
     const int npairs = (nkb + 1) / 2;
     const int BKV = (int)(B * KVH);
-    fa_bwd_dkdv_kernel<HD, DT><<<dim3(npairs * BKV), dim3(256), 0, st>>>(
+    fa_bwd_dkdv_kernel<HD, DT><<<dim3(npairs * BKV * w.nsplit), dim3(256), 0, st>>>(
         (const u16*)q, (const u16*)k, (const u16*)v, (const u16*)dO, w.nL, w.nD, (u16*)dk, (u16*)dv, BKV, (int)H,
-        (int)KVH, (int)T, nkb, nqt, scale * kLog2e, scale, lq, lk);
-    return launch_status("fa_bwd_dkdv_kernel");
+        (int)KVH, (int)T, nkb, nqt, scale * kLog2e, scale, lq, lk, w.nsplit, w.part);
+    if (int e = launch_status("fa_bwd_dkdv_kernel")) return e;
+    if (w.nsplit == 1) return 0;
+    const int64_t n4 = 2 * (int64_t)BKV * T * HD / 4;
+    const int blocks = (int)std::min<int64_t>((n4 + 255) / 256, 2048);
+    fa_bwd_dkdv_sum_kernel<DT><<<dim3(blocks), dim3(256), 0, st>>>(w.part, (u16*)dk, (u16*)dv, w.nsplit, BKV, (int)KVH,
+                                                                   (int)T, HD, lk);
+    return launch_status("fa_bwd_dkdv_sum_kernel");
 }
 
 template <int HD, int DT>
@@ -1092,10 +1162,10 @@ int take_layout(const int64_t* strides, int64_t heads, int64_t T, int64_t D, con
     return 0;
 }
 
-int check_ws(void* workspace, size_t workspace_bytes, int64_t B, int64_t H, int64_t T) {
+int check_ws(void* workspace, size_t workspace_bytes, int64_t B, int64_t H, int64_t KVH, int64_t T, int64_t D) {
     if (!workspace) return fail(-1, "null workspace");
     if (((uintptr_t)workspace & 255u) != 0) return fail(-1, "workspace must be 256-byte aligned");
-    const size_t need = carve(nullptr, B, H, T).bytes;
+    const size_t need = carve(nullptr, B, H, KVH, T, D).bytes;
     if (workspace_bytes < need) return fail(-1, "workspace too small: %zu bytes given, %zu needed", workspace_bytes, need);
     return 0;
 }
@@ -1111,13 +1181,11 @@ int check_ws(void* workspace, size_t workspace_bytes, int64_t B, int64_t H, int6
 
 NNFA_API const char* nn_fa_last_error(void) { return g_last_error.c_str(); }
 
-NNFA_API int nn_fa_abi_version(void) { return 6; }
+NNFA_API int nn_fa_abi_version(void) { return 7; }
 
 NNFA_API size_t nn_fa_bwd_workspace_size(int64_t B, int64_t H, int64_t KVH, int64_t T, int64_t D) {
-    (void)KVH;
-    (void)D;
-    if (B < 0 || H < 0 || T < 0) return 0;
-    return carve(nullptr, B, H, T).bytes;
+    if (B < 0 || H < 0 || KVH < 0 || T < 0 || D < 0) return 0;
+    return carve(nullptr, B, H, KVH, T, D).bytes;
 }
 
 namespace {
@@ -1145,8 +1213,8 @@ int bwd_prologue(const void* workspace, size_t workspace_bytes, int64_t B, int64
     g_last_error.clear();
     if (int e = check_dims(B, H, KVH, T, D, dtype)) return e;
     if (B == 0 || T == 0) return 1;  // nothing to do
-    if (int e = check_ws((void*)workspace, workspace_bytes, B, H, T)) return e;
-    *w = carve((void*)workspace, B, H, T);
+    if (int e = check_ws((void*)workspace, workspace_bytes, B, H, KVH, T, D)) return e;
+    *w = carve((void*)workspace, B, H, KVH, T, D);
     *lq = contiguous(H, T, D);
     *lk = contiguous(KVH, T, D);
     if (qo_strides)
@@ -1169,7 +1237,7 @@ int pre_entry(const void* o, const void* dO, const float* lse, void* workspace, 
     return NNFA_DISPATCH(pre_impl, D, dtype, o, dO, lse, w, B, H, KVH, T, scale, lq, (hipStream_t)stream);
 }
 
-int dkdv_entry(const void* q, const void* k, const void* v, const void* dO, const void* workspace,
+int dkdv_entry(const void* q, const void* k, const void* v, const void* dO, void* workspace,
                size_t workspace_bytes, void* dk, void* dv, int64_t B, int64_t H, int64_t KVH, int64_t T, int64_t D,
                int dtype, float scale, const int64_t* qo_strides, const int64_t* kv_strides, void* stream) {
     Workspace w;
@@ -1240,7 +1308,7 @@ NNFA_API int nn_fa_bwd_pre(const void* o, const void* dO, const float* lse, void
     return pre_entry(o, dO, lse, workspace, workspace_bytes, B, H, KVH, T, D, dtype, scale, nullptr, stream);
 }
 
-NNFA_API int nn_fa_bwd_dkdv(const void* q, const void* k, const void* v, const void* dO, const void* workspace,
+NNFA_API int nn_fa_bwd_dkdv(const void* q, const void* k, const void* v, const void* dO, void* workspace,
                             size_t workspace_bytes, void* dk, void* dv, int64_t B, int64_t H, int64_t KVH, int64_t T,
                             int64_t D, int dtype, float scale, void* stream) {
     return dkdv_entry(q, k, v, dO, workspace, workspace_bytes, dk, dv, B, H, KVH, T, D, dtype, scale, nullptr, nullptr,

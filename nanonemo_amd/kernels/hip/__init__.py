@@ -71,7 +71,7 @@ SIGNATURES: dict[str, tuple] = {
     "nn_rmsnorm_last_error": (ctypes.c_char_p, []),
 }
 
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 
 @cache

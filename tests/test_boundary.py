@@ -42,12 +42,28 @@ def test_abi_version():
     assert lib().nn_fa_abi_version() == ABI_VERSION
 
 
-def test_workspace_size():
+def _dkdv_split(B, H, KVH, T):
+    """Blocks sharing one dK/dV unit pair: 1 when the B*KVH*ceil(nkb/2) pairs fill 256 CUs, else up to 16,
+    keeping at least 8 of a pair's (H/KVH)*(nkb+1) iterations per split."""
+    nkb = (T + 63) // 64
+    base = B * KVH * ((nkb + 1) // 2)
+    if base <= 0 or base >= 256:
+        return 1
+    return max(1, min(16, -(-256 // base), (H // KVH) * (nkb + 1) // 8))
+
+
+@pytest.mark.parametrize(
+    "B, H, KVH, T, D, split",
+    [(8, 12, 4, 1024, 64, 1), (32, 12, 4, 1024, 64, 1), (8, 12, 1, 1024, 64, 4), (1, 12, 4, 1024, 64, 6),
+     (1, 12, 4, 256, 64, 1), (2, 12, 1, 1024, 64, 16), (1, 8, 8, 700, 32, 1), (1, 1, 1, 1, 32, 1)],
+)
+def test_workspace_size(B, H, KVH, T, D, split):
     L = lib()
-    B, H, KVH, T, D = 8, 12, 4, 1024, 64
+    assert _dkdv_split(B, H, KVH, T) == split
     vec = 4 * B * H * T  # -rowsum(dO * o) and -lse/scale, fp32 per query row
     rnd = lambda n: (n + 255) // 256 * 256  # noqa: E731
-    assert L.nn_fa_bwd_workspace_size(B, H, KVH, T, D) == 2 * rnd(vec)
+    part = split * 2 * 4 * B * KVH * T * D if split > 1 else 0  # fp32 dK / dV partials of each split
+    assert L.nn_fa_bwd_workspace_size(B, H, KVH, T, D) == 2 * rnd(vec) + rnd(part)
     assert L.nn_fa_bwd_workspace_size(0, H, KVH, T, D) == 0
 
 

@@ -142,6 +142,30 @@ def test_deterministic_forward():
     assert torch.equal(fa.flash_attn(q, k, v), fa.flash_attn(q, k, v))
 
 
+# Shapes whose dK/dV work units (B * KVH * ceil(T / 128)) are too few to fill the chip, so that each unit
+# pair is split over several blocks whose fp32 partials are summed afterwards (16 and 9 splits here).
+SPLIT = [(2, 12, 1, 1024, 64), (1, 12, 2, 700, 32)]
+
+
+@pytest.mark.parametrize("B, H, KVH, T, hd", SPLIT)
+def test_split_dkdv_matches_oracle(B, H, KVH, T, hd):
+    dtype = torch.bfloat16
+    q, k, v, do = make_inputs(B, H, KVH, T, hd, dtype, seed=11)
+    _check(_run(q, k, v, do), _oracle(q, k, v, do), dtype, f"split {(B, H, KVH, T, hd)}")
+
+
+def test_deterministic_backward():
+    # The backward has no atomics: the split dK/dV partials are summed in split order, the unsplit ones
+    # through LDS in wave order, so repeated calls agree bit for bit.
+    fa = _fa()
+    for shape in (SPLIT[0], (8, 12, 4, 1024, 64)):
+        q, k, v, do = (t.to(DEV) for t in make_inputs(*shape, torch.bfloat16, seed=3))
+        o, lse = fa._flash_attn(q, k, v)
+        g1 = fa._flash_attn_bwd(do, q, k, v, o, lse)
+        g2 = fa._flash_attn_bwd(do, q, k, v, o, lse)
+        assert all(torch.equal(a, b) for a, b in zip(g1, g2)), shape
+
+
 def test_opcheck():
     fa = _fa()
     for dtype in (torch.float16, torch.bfloat16):

@@ -3,7 +3,8 @@ common.py:30-54, and that compile(mode="reduce-overhead") relies on, trainer.py:
 
 The library allocates, frees, synchronises and memsets nothing, so its calls can be captured. Here the
 calls themselves are captured with torch.cuda.graph on buffers allocated beforehand (no autograd inside
-the capture): one nn_fa_fwd + nn_fa_bwd pair, and the RoPE and fused add + RMSNorm kernels beside it.
+the capture): one nn_fa_fwd + nn_fa_bwd pair (also at a shape whose dK/dV work is split, which adds the
+partial-sum kernel), and the RoPE and fused add + RMSNorm kernels beside it.
 Each graph is replayed several times with eager work and synchronisations in between, outputs poisoned
 before every replay; every replay must equal the eager result bit for bit.
 """
@@ -45,11 +46,11 @@ def _replays_match(launch, outs, n=4):
         del junk
 
 
-def test_captured_fwd_bwd_c_abi_calls_replay_bit_identically():
+@pytest.mark.parametrize("B, H, KVH, T, D", [(2, 12, 4, 256, 64), (2, 12, 1, 1024, 64)])  # the second splits dK/dV
+def test_captured_fwd_bwd_c_abi_calls_replay_bit_identically(B, H, KVH, T, D):
     from nanonemo_amd.kernels.hip import DTYPE_BF16, check, lib
 
     L = lib()
-    B, H, KVH, T, D = 2, 12, 4, 256, 64
     print(f"\n[case] graph capture of nn_fa_fwd + nn_fa_bwd B={B} H={H} KVH={KVH} T={T} D={D}", flush=True)
     q, k, v, do = (t.cuda() for t in make_inputs(B, H, KVH, T, D, torch.bfloat16, seed=2))
     o, dq = torch.empty_like(q), torch.empty_like(q)
