@@ -529,7 +529,7 @@ __global__ __launch_bounds__(256) void fa_bwd_pre_kernel(const u16* __restrict__
 //   P = exp2(S' * sl2), dS = P dP'
 //   dV^T += dO^T P, dK^T += Q^T dS             (A = columns of the Q / dO tiles, B = P / dS registers)
 // ------------------------------------------------------------------------------------------
-template <int HD, int DT>
+template <int HD, int DT, int WPP>
 __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(
     const u16* __restrict__ Q, const u16* __restrict__ K, const u16* __restrict__ V, const u16* __restrict__ dO,
     const float* __restrict__ nLvec, const float* __restrict__ nDvec, u16* __restrict__ dK, u16* __restrict__ dV,
@@ -537,6 +537,8 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(
     float* __restrict__ part) {
     using E = Elem<DT>;
     constexpr int BNK = 64, BM = 64, NW = 4, NSL = BNK / 32;
+    constexpr int PPB = NW / WPP;  // unit pairs per block: waves WPP p .. WPP p + WPP - 1 share pair p
+    static_assert(WPP == 1 || WPP == 2 || WPP == 4, "waves per unit pair");
     constexpr int NS = HD / 16;
     constexpr int ND = HD / 32;
     constexpr int QT = BM * HD;  // elements of one Q or dO tile
@@ -550,14 +552,18 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(
     __shared__ __attribute__((aligned(16))) float lA[NW * 2 * BM];  // per wave: -lse/scale | -D
     __shared__ __attribute__((aligned(16))) float lB[NW * 2 * BM];
 
-    const int nbase = BKV * ((nkb + 1) / 2);  // blocks of one split
+    const int nbk = (BKV + PPB - 1) / PPB;   // blocks per unit-pair index (and split)
+    const int nbase = nbk * ((nkb + 1) / 2);  // blocks of one split
     const int sidx = blockIdx.x / nbase;      // this block's split
     const int bid = blockIdx.x - sidx * nbase;
-    const int bk = bid % BKV;
-    const int pj = bid / BKV;
-    const int b = bk / KVH, kvh = bk - b * KVH, group = H / KVH;
+    const int bgrp = bid % nbk;               // the block's pairs are (batch, KV head) bgrp PPB .. + PPB - 1
+    const int pj = bid / nbk;
     const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
     const int wave = tid >> 6;  // a uniform copy in an SGPR costs this kernel more than it saves
+    const int wp = wave % WPP;  // this wave's place among its pair's waves
+    const int bk = bgrp * PPB + wave / WPP;  // past BKV (the last block): the wave idles but keeps the barriers
+    const bool active = bk < BKV;
+    const int b = bk / KVH, kvh = bk - b * KVH, group = H / KVH;
     const DmaOffs<HD, BM, 1> dfo = dma_offsets<HD, BM, 1>(lane, 0, lq.st);
     // This split's iterations [first, end) of a unit with n of them.
     auto first_of = [&](int n) { return (int)((int64_t)sidx * n / nsplit); };
@@ -606,10 +612,10 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(
     // The first unit's K / V and first tiles; each later unit's are issued before the previous unit's
     // reduction, so that their latency overlaps it.
     const int nunits = nkb - 1 - pj > pj ? 2 : 1;  // an odd unit count leaves the middle unit alone
-    load_kv(pj * BNK);
-    {
+    if (active) {
+        load_kv(pj * BNK);
         const int n0 = group * (nqt - pj), i0 = first_of(n0);
-        if (wave < end_of(n0) - i0) issue_it(i0 + wave, pj, nqt - pj, qA, oA, lA);
+        if (wp < end_of(n0) - i0) issue_it(i0 + wp, pj, nqt - pj, qA, oA, lA);
     }
 
     for (int ui = 0; ui < nunits; ++ui) {
@@ -617,7 +623,7 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(
         const int kb0 = unit * BNK;
         const int qt_first = unit, nq = nqt - qt_first, niter = group * nq;
         const int ifirst = first_of(niter), nsp = end_of(niter) - ifirst;  // this split's iterations
-        const int nmine = wave < nsp ? (nsp - wave + NW - 1) / NW : 0;  // iterations ifirst + wave + NW j
+        const int nmine = active && wp < nsp ? (nsp - wp + WPP - 1) / WPP : 0;  // iterations ifirst + wp + WPP j
 
         f32x16 dk[NSL][ND], dv[NSL][ND];
 #pragma unroll
@@ -756,39 +762,43 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(
         // Double-buffered: this wave's iteration j uses buffer j % 2 while j + 1 streams into the other.
         // The DMA into a buffer is issued only after this wave's own reads of it (iteration j - 1)
         // have returned, which their use by the MFMAs guarantees.
-        for (int j = 0; j < nmine; j += 2) {  // iteration ifirst + wave is already in flight into buffer A
-            const int itn = ifirst + wave + NW * j;
+        for (int j = 0; j < nmine; j += 2) {  // iteration ifirst + wp is already in flight into buffer A
+            const int itn = ifirst + wp + WPP * j;
             wait_vmem();  // this iteration's tiles, copied during the previous one
             if (j + 1 < nmine)
-                run(std::true_type{}, itn, qA, oA, lA, itn + NW, qB, oB, lB);
+                run(std::true_type{}, itn, qA, oA, lA, itn + WPP, qB, oB, lB);
             else
                 run(std::false_type{}, itn, qA, oA, lA, 0, qB, oB, lB);
             if (j + 1 >= nmine) break;
             wait_vmem();
             if (j + 2 < nmine)
-                run(std::true_type{}, itn + NW, qB, oB, lB, itn + 2 * NW, qA, oA, lA);
+                run(std::true_type{}, itn + WPP, qB, oB, lB, itn + 2 * WPP, qA, oA, lA);
             else
-                run(std::false_type{}, itn + NW, qB, oB, lB, 0, qA, oA, lA);
+                run(std::false_type{}, itn + WPP, qB, oB, lB, 0, qA, oA, lA);
         }
 
         // Every wave is done with its tiles and its DMA: the tile space is free.
         __syncthreads();
         if (ui + 1 < nunits) {  // the next unit's K / V and first tiles (into the A buffers), in flight during
             const int un = nkb - 1 - pj;  // the reduction, which uses only the B buffers
-            load_kv(un * BNK);
-            const int n1 = group * (nqt - un), i1 = first_of(n1);
-            if (wave < end_of(n1) - i1) issue_it(i1 + wave, un, nqt - un, qA, oA, lA);
+            if (active) {
+                load_kv(un * BNK);
+                const int n1 = group * (nqt - un), i1 = first_of(n1);
+                if (wp < end_of(n1) - i1) issue_it(i1 + wp, un, nqt - un, qA, oA, lA);
+            }
         }
-        // Sum the 4 waves' partial dK^T, then dV^T (lane = key, element i = column
+        // Sum each pair's WPP partial dK^T, then dV^T (lane = key, element i = column
         // 32dt + (i/4)*8 + 4hh + i%4) through LDS in the B buffers, which the next unit's first tiles
-        // leave alone: [64 keys][HD] fp32 per wave, 16-byte chunks XOR-swizzled by row.
+        // leave alone: [64 keys][HD] fp32 per wave, 16-byte chunks XOR-swizzled by row. Each pair's
+        // partials are added in wave order.
         // The epilogue's addressing is derived from a copy of tid the compiler cannot see through,
         // so it is computed here rather than hoisted to the kernel entry and spilled across the loop.
         int etid;
         __asm__ volatile("v_mov_b32 %0, %1" : "=v"(etid) : "v"(tid));
         float* const st0 = reinterpret_cast<float*>(qB);  // waves 0, 1 stage in qB, waves 2, 3 in oB
+        auto staged = [&](int w) { return (w < 2 ? st0 : reinterpret_cast<float*>(oB)) + (w & 1) * BNK * HD; };
         auto reduce_store = [&](const f32x16 (&acc)[NSL][ND], float mul, u16* out, int which) {
-            float* mine = (wave < 2 ? st0 : reinterpret_cast<float*>(oB)) + (wave & 1) * BNK * HD;
+            float* mine = staged(wave);
 #pragma unroll
             for (int sl = 0; sl < NSL; ++sl) {
                 const int kr = 32 * sl + l32;
@@ -805,22 +815,23 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(
             // flight; its loop waits for them (vmcnt) before reading either.
             barrier_lds();
 #pragma unroll
-            for (int k = 0; k < BNK * CH4 / 256; ++k) {
+            for (int k = 0; k < PPB * BNK * CH4 / 256; ++k) {
                 const int it = etid + 256 * k;
-                const int row = it / CH4, c = it - row * CH4;
+                const int ps = it / (BNK * CH4), rem = it - ps * (BNK * CH4);  // pair ps of the block
+                const int row = rem / CH4, c = rem - row * CH4;
                 const int off = row * HD + 4 * ((c ^ row) & (CH4 - 1));
-                const float* s2 = reinterpret_cast<const float*>(oB);
-                f32x4 sum = *reinterpret_cast<const f32x4*>(st0 + off);
-                sum += *reinterpret_cast<const f32x4*>(st0 + BNK * HD + off);
-                sum += *reinterpret_cast<const f32x4*>(s2 + off);
-                sum += *reinterpret_cast<const f32x4*>(s2 + BNK * HD + off);
+                f32x4 sum = *reinterpret_cast<const f32x4*>(staged(ps * WPP) + off);
+#pragma unroll
+                for (int m = 1; m < WPP; ++m) sum += *reinterpret_cast<const f32x4*>(staged(ps * WPP + m) + off);
                 sum *= mul;
-                if (kb0 + row < T) {
+                const int pbk = bgrp * PPB + ps;
+                if (pbk < BKV && kb0 + row < T) {
                     if (nsplit == 1) {
-                        u16* dst = out + kvoff + (size_t)(kb0 + row) * lk.st + 4 * c;
+                        const int pb = pbk / KVH;
+                        u16* dst = out + lk.at(pb, pbk - pb * KVH) + (size_t)(kb0 + row) * lk.st + 4 * c;
                         *reinterpret_cast<u32x2*>(dst) = u32x2{E::pack2(sum[0], sum[1]), E::pack2(sum[2], sum[3])};
                     } else {  // this split's partial: part[split][dK | dV][bk][key][HD]
-                        float* dst = part + (((size_t)sidx * 2 + which) * BKV + bk) * T * HD + (size_t)(kb0 + row) * HD + 4 * c;
+                        float* dst = part + (((size_t)sidx * 2 + which) * BKV + pbk) * T * HD + (size_t)(kb0 + row) * HD + 4 * c;
                         *reinterpret_cast<f32x4*>(dst) = sum;
                     }
                 }
@@ -1081,6 +1092,18 @@ int dkdv_split(int64_t B, int64_t H, int64_t KVH, int64_t T) {
     return (int)std::max<int64_t>(1, std::min({kDkdvMaxSplit, by_fill, by_work}));
 }
 
+// Waves sharing one unit pair (1, 2 or 4; see dkdv_impl). Splitting (dkdv_split > 1) needs 4. Fewer waves
+// per pair pay off while a pair's (query head, query tile) iterations are few enough that its fixed costs
+// weigh (measured: 8-24 % faster at up to about 200 iterations); long pairs amortise those costs anyway,
+// and four waves on one pair keep its Q / dO tiles in L2 (B=1, T=16384: two waves per pair 8 % slower).
+constexpr int64_t kDkdvFewWavesMaxIters = 300;
+int dkdv_waves_per_pair(int64_t B, int64_t H, int64_t KVH, int64_t T) {
+    if (B <= 0 || KVH <= 0 || H < KVH || T <= 0) return 4;
+    const int64_t nkb = (T + 63) / 64, pairs = B * KVH * ((nkb + 1) / 2);
+    if ((H / KVH) * (nkb + 1) > kDkdvFewWavesMaxIters) return 4;
+    return pairs >= 3 * kDkdvFill ? 1 : (pairs >= 2 * kDkdvFill ? 2 : 4);
+}
+
 Workspace carve(void* base, int64_t B, int64_t H, int64_t KVH, int64_t T, int64_t D) {
     const size_t vec = round256(4 * (size_t)B * H * T);
     Workspace w;
@@ -1120,9 +1143,22 @@ int dkdv_impl(const void* q, const void* k, const void* v, const void* dO, const
     const int nqt = nkb;                   // 64-row query tiles
     const int npairs = (nkb + 1) / 2;
     const int BKV = (int)(B * KVH);
-    fa_bwd_dkdv_kernel<HD, DT><<<dim3(npairs * BKV * w.nsplit), dim3(256), 0, st>>>(
-        (const u16*)q, (const u16*)k, (const u16*)v, (const u16*)dO, w.nL, w.nD, (u16*)dk, (u16*)dv, BKV, (int)H,
-        (int)KVH, (int)T, nkb, nqt, scale * kLog2e, scale, lq, lk, w.nsplit, w.part);
+    // Waves per unit pair: 4 while the pairs do not fill two blocks per CU; with more pairs, fewer waves
+    // share each pair (a block then hosts 2 or 4 pairs), so that the per-unit costs (loads, barrier,
+    // reduction) are paid by fewer, longer blocks.
+    const int wpp = dkdv_waves_per_pair(B, H, KVH, T);
+    auto launch = [&](auto kern, int ppb) {
+        const int nbk = (BKV + ppb - 1) / ppb;
+        kern<<<dim3(nbk * npairs * w.nsplit), dim3(256), 0, st>>>(
+            (const u16*)q, (const u16*)k, (const u16*)v, (const u16*)dO, w.nL, w.nD, (u16*)dk, (u16*)dv, BKV, (int)H,
+            (int)KVH, (int)T, nkb, nqt, scale * kLog2e, scale, lq, lk, w.nsplit, w.part);
+    };
+    if (wpp == 1)
+        launch(fa_bwd_dkdv_kernel<HD, DT, 1>, 4);
+    else if (wpp == 2)
+        launch(fa_bwd_dkdv_kernel<HD, DT, 2>, 2);
+    else
+        launch(fa_bwd_dkdv_kernel<HD, DT, 4>, 1);
     if (int e = launch_status("fa_bwd_dkdv_kernel")) return e;
     if (w.nsplit == 1) return 0;
     const int64_t n4 = 2 * (int64_t)BKV * T * HD / 4;

@@ -154,6 +154,19 @@ def test_split_dkdv_matches_oracle(B, H, KVH, T, hd):
     _check(_run(q, k, v, do), _oracle(q, k, v, do), dtype, f"split {(B, H, KVH, T, hd)}")
 
 
+# Shapes with enough unit pairs that fewer waves share each (B*KVH*ceil(T/128) >= 768: one wave per pair, four
+# pairs per block; >= 512: two waves per pair). The second leaves two waves of its last block idle (130
+# pairs), the third one pair in its last block (91 pairs of two).
+WPP = [(12, 8, 8, 1024, 32), (65, 4, 2, 700, 32), (91, 2, 1, 700, 32)]
+
+
+@pytest.mark.parametrize("B, H, KVH, T, hd", WPP)
+def test_fewer_waves_per_unit_pair_matches_oracle(B, H, KVH, T, hd):
+    dtype = torch.bfloat16
+    q, k, v, do = make_inputs(B, H, KVH, T, hd, dtype, seed=13)
+    _check(_run(q, k, v, do), _oracle(q, k, v, do), dtype, f"waves per pair {(B, H, KVH, T, hd)}")
+
+
 def test_deterministic_backward():
     # The backward has no atomics: the split dK/dV partials are summed in split order, the unsplit ones
     # through LDS in wave order, so repeated calls agree bit for bit.
