@@ -566,8 +566,10 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(
     const int b = bk / KVH, kvh = bk - b * KVH, group = H / KVH;
     const DmaOffs<HD, BM, 1> dfo = dma_offsets<HD, BM, 1>(lane, 0, lq.st);
     // This split's iterations [first, end) of a unit with n of them.
-    auto first_of = [&](int n) { return (int)((int64_t)sidx * n / nsplit); };
-    auto end_of = [&](int n) { return (int)((int64_t)(sidx + 1) * n / nsplit); };
+    // 32-bit: the host splits only units whose (sidx + 1) n stays below 2^31 (dkdv_split).
+    const uint32_t su = __builtin_amdgcn_readfirstlane(sidx), nsu = __builtin_amdgcn_readfirstlane(nsplit);
+    auto first_of = [&](int n) { return (int)(su * (uint32_t)n / nsu); };
+    auto end_of = [&](int n) { return (int)((su + 1) * (uint32_t)n / nsu); };
     const int g16 = (lane >> 4) & 1;
     const size_t kvoff = lk.at(b, kvh);
 
@@ -814,11 +816,13 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(
             // LDS-only barriers: the loads and DMA of the next unit (K / V registers, A buffers) stay in
             // flight; its loop waits for them (vmcnt) before reading either.
             barrier_lds();
+            constexpr int KP = BNK * CH4 / 256;  // passes of the 256 threads over one pair's [64][HD] sums
+            static_assert(BNK * CH4 % 256 == 0, "whole passes per pair");
 #pragma unroll
-            for (int k = 0; k < PPB * BNK * CH4 / 256; ++k) {
-                const int it = etid + 256 * k;
-                const int ps = it / (BNK * CH4), rem = it - ps * (BNK * CH4);  // pair ps of the block
-                const int row = rem / CH4, c = rem - row * CH4;
+            for (int k = 0; k < PPB * KP; ++k) {
+                const int ps = k / KP;  // pair ps of the block: fixed per unrolled pass, so pbk stays scalar
+                const uint32_t rem = (uint32_t)etid + 256u * (k % KP);
+                const int row = rem / CH4, c = rem % CH4;
                 const int off = row * HD + 4 * ((c ^ row) & (CH4 - 1));
                 f32x4 sum = *reinterpret_cast<const f32x4*>(staged(ps * WPP) + off);
 #pragma unroll
@@ -1088,6 +1092,7 @@ int dkdv_split(int64_t B, int64_t H, int64_t KVH, int64_t T) {
     if (B <= 0 || KVH <= 0 || H < KVH || T <= 0) return 1;
     const int64_t nkb = (T + 63) / 64, base = B * KVH * ((nkb + 1) / 2);
     if (base >= kDkdvFill) return 1;
+    if ((H / KVH) * nkb * kDkdvMaxSplit >= ((int64_t)1 << 31)) return 1;  // the kernel's 32-bit split bounds
     const int64_t by_fill = (kDkdvFill + base - 1) / base, by_work = (H / KVH) * (nkb + 1) / kDkdvMinIters;
     return (int)std::max<int64_t>(1, std::min({kDkdvMaxSplit, by_fill, by_work}));
 }

@@ -44,10 +44,11 @@ def test_abi_version():
 
 def _dkdv_split(B, H, KVH, T):
     """Blocks sharing one dK/dV unit pair: 1 when the B*KVH*ceil(nkb/2) pairs fill 256 CUs, else up to 16,
-    keeping at least 8 of a pair's (H/KVH)*(nkb+1) iterations per split."""
+    keeping at least 8 of a pair's (H/KVH)*(nkb+1) iterations per split, and none where 16 times a unit's
+    (H/KVH)*nkb iterations would overflow the kernel's 32-bit split bounds."""
     nkb = (T + 63) // 64
     base = B * KVH * ((nkb + 1) // 2)
-    if base <= 0 or base >= 256:
+    if base <= 0 or base >= 256 or (H // KVH) * nkb * 16 >= 2**31:
         return 1
     return max(1, min(16, -(-256 // base), (H // KVH) * (nkb + 1) // 8))
 
@@ -55,7 +56,8 @@ def _dkdv_split(B, H, KVH, T):
 @pytest.mark.parametrize(
     "B, H, KVH, T, D, split",
     [(8, 12, 4, 1024, 64, 1), (32, 12, 4, 1024, 64, 1), (8, 12, 1, 1024, 64, 4), (1, 12, 4, 1024, 64, 6),
-     (1, 12, 4, 256, 64, 1), (2, 12, 1, 1024, 64, 16), (1, 8, 8, 700, 32, 1), (1, 1, 1, 1, 32, 1)],
+     (1, 12, 4, 256, 64, 1), (2, 12, 1, 1024, 64, 16), (1, 8, 8, 700, 32, 1), (1, 1, 1, 1, 32, 1),
+     (1, 1 << 27, 1, 64, 32, 1), (1, (1 << 27) - 8, 1, 64, 32, 16)],
 )
 def test_workspace_size(B, H, KVH, T, D, split):
     L = lib()
