@@ -542,9 +542,7 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(
     constexpr int NS = HD / 16;
     constexpr int ND = HD / 32;
     constexpr int QT = BM * HD;  // elements of one Q or dO tile
-    constexpr int CH4 = HD / 4;  // 16-byte fp32 chunks per staged gradient row
     static_assert(BNK == BM, "a unit's first query tile is its own index");
-    static_assert(2 * NW * QT * 2 >= NW * BNK * HD * 4, "one gradient's staging fits in the B tile buffers");
     __shared__ __attribute__((aligned(16))) u16 qA[NW * QT];
     __shared__ __attribute__((aligned(16))) u16 oA[NW * QT];
     __shared__ __attribute__((aligned(16))) u16 qB[NW * QT];
@@ -594,17 +592,20 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(
             }
         }
     };
-    // DMA iteration itn of the unit whose query tiles start at tile qtf (nqq of them: iteration itn is
-    // query head itn / nqq of the group, tile qtf + itn % nqq) into this wave's slot: the Q / dO tiles
-    // and the -lse/scale, -D vectors.
-    auto issue_it = [&](int itn, int qtf, int nqq, u16* qs, u16* os, float* ls) {
+    // Iteration itn of the unit whose query tiles start at tile qtf: query head iter_head of the group,
+    // query tile iter_tile. With several waves per pair head-minor, so that the group's diagonal
+    // iterations, which carry the mask, go to different waves; with one wave head-major.
+    auto iter_head = [&](int itn, int qtf) { return WPP > 1 ? itn % group : itn / (nqt - qtf); };
+    auto iter_tile = [&](int itn, int qtf) { return qtf + (WPP > 1 ? itn / group : itn % (nqt - qtf)); };
+    // DMA iteration itn into this wave's slot: the Q / dO tiles and the -lse/scale, -D vectors.
+    auto issue_it = [&](int itn, int qtf, u16* qs, u16* os, float* ls) {
         // Wave-uniform in fact; made uniform for the compiler only here, so that the tile addressing is
         // scalar without keeping scalar copies alive across the whole kernel.
         const int itu = __builtin_amdgcn_readfirstlane(itn), wu = __builtin_amdgcn_readfirstlane(wave);
-        const int hq = kvh * group + itu / nqq;
+        const int hq = kvh * group + iter_head(itu, qtf);
         const size_t ro = ((size_t)b * H + hq) * T;  // first row of the head's [T] vectors
         const size_t qo = lq.at(b, hq);
-        const int q0 = (qtf + itu % nqq) * BM;
+        const int q0 = iter_tile(itu, qtf) * BM;
         dma_rows<HD, BM, 1>(Q + qo, lq.st, q0, T, qs + wu * QT, 0, dfo);
         dma_rows<HD, BM, 1>(dO + qo, lq.st, q0, T, os + wu * QT, 0, dfo);
         const uint32_t lo = (uint32_t)min(lane, T - 1 - q0) * 4;  // rows past T repeat row T - 1
@@ -617,7 +618,7 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(
     if (active) {
         load_kv(pj * BNK);
         const int n0 = group * (nqt - pj), i0 = first_of(n0);
-        if (wp < end_of(n0) - i0) issue_it(i0 + wp, pj, nqt - pj, qA, oA, lA);
+        if (wp < end_of(n0) - i0) issue_it(i0 + wp, pj, qA, oA, lA);
     }
 
     for (int ui = 0; ui < nunits; ++ui) {
@@ -634,8 +635,8 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(
             for (int dt = 0; dt < ND; ++dt) dk[sl][dt] = dv[sl][dt] = f32x16{};
 
         // Iteration itn -> 64-row query tile.
-        auto qbase_of = [&](int itn) { return (qt_first + itn % nq) * BM; };
-        auto issue = [&](int itn, u16* qs, u16* os, float* ls) { issue_it(itn, qt_first, nq, qs, os, ls); };
+        auto qbase_of = [&](int itn) { return iter_tile(itn, qt_first) * BM; };
+        auto issue = [&](int itn, u16* qs, u16* os, float* ls) { issue_it(itn, qt_first, qs, os, ls); };
         // One 64-query iteration: two 32-query steps, each against both 32-key slabs.
         // MASK: the iteration crosses the diagonal or T (a separate instantiation, so that unmasked
         // iterations carry no per-element selects).
@@ -779,68 +780,76 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(
                 run(std::false_type{}, itn + WPP, qB, oB, lB, 0, qA, oA, lA);
         }
 
-        // Every wave is done with its tiles and its DMA: the tile space is free.
-        __syncthreads();
-        if (ui + 1 < nunits) {  // the next unit's K / V and first tiles (into the A buffers), in flight during
-            const int un = nkb - 1 - pj;  // the reduction, which uses only the B buffers
-            if (active) {
-                load_kv(un * BNK);
-                const int n1 = group * (nqt - un), i1 = first_of(n1);
-                if (wp < end_of(n1) - i1) issue_it(i1 + wp, un, nqt - un, qA, oA, lA);
-            }
+        // This wave is done with its tiles, its copies have landed (its last iteration issued none) and
+        // its K / V registers are free: it issues the next unit's K / V loads and first tiles (into its A
+        // slots) now, while it waits for the slower waves, and they stay in flight through the reduction,
+        // which uses only the B buffers. The next unit's loop waits for them (vmcnt) before reading either.
+        if (ui + 1 < nunits && active) {
+            const int un = nkb - 1 - pj;
+            load_kv(un * BNK);
+            const int n1 = group * (nqt - un), i1 = first_of(n1);
+            if (wp < end_of(n1) - i1) issue_it(i1 + wp, un, qA, oA, lA);
         }
-        // Sum each pair's WPP partial dK^T, then dV^T (lane = key, element i = column
-        // 32dt + (i/4)*8 + 4hh + i%4) through LDS in the B buffers, which the next unit's first tiles
-        // leave alone: [64 keys][HD] fp32 per wave, 16-byte chunks XOR-swizzled by row. Each pair's
-        // partials are added in wave order.
-        // The epilogue's addressing is derived from a copy of tid the compiler cannot see through,
-        // so it is computed here rather than hoisted to the kernel entry and spilled across the loop.
-        int etid;
-        __asm__ volatile("v_mov_b32 %0, %1" : "=v"(etid) : "v"(tid));
-        float* const st0 = reinterpret_cast<float*>(qB);  // waves 0, 1 stage in qB, waves 2, 3 in oB
-        auto staged = [&](int w) { return (w < 2 ? st0 : reinterpret_cast<float*>(oB)) + (w & 1) * BNK * HD; };
+        if constexpr (WPP > 1) barrier_lds();  // every wave's loop is done: the B buffers can take the staged sums
+        // Sum each pair's WPP partial dK^T, then dV^T, and store the sums. A wave's partial is NCK chunks of
+        // 1 KB: chunk (sl, dt, g) holds accumulator elements 4g .. 4g + 3 of acc[sl][dt] in every lane
+        // (lane = key 32 sl + l32, element 4g + e = column 32 dt + 8g + 4hh + e). Chunk (sl, dt, g) belongs
+        // to wave g % WPP of the pair: the pair's other waves stage their copies of it in LDS (the B
+        // buffers, which the next unit's first tiles leave alone), and the owner adds them and its own in
+        // wave order and stores the sum. With one wave per pair nothing is staged and no wave waits for
+        // another. The LDS-only barriers leave the next unit's loads in flight.
+        constexpr int NCK = NSL * ND * 4;
+        static_assert(2 * NCK * 1024 <= NW * QT * 2, "two waves' staged chunks fit in one B tile buffer");
+        auto slot = [&](int w, int c) {  // wave w's staged copy of chunk c: waves 0, 1 in qB, waves 2, 3 in oB
+            return reinterpret_cast<f32x4*>(w < 2 ? qB : oB) + ((w & 1) * NCK + c) * 64 + lane;
+        };
         auto reduce_store = [&](const f32x16 (&acc)[NSL][ND], float mul, u16* out, int which) {
-            float* mine = staged(wave);
+            auto chunk = [&](int c) {
+                const f32x16& a = acc[c / (4 * ND)][c / 4 % ND];
+                const int g = c % 4;
+                return f32x4{a[4 * g], a[4 * g + 1], a[4 * g + 2], a[4 * g + 3]};
+            };
+            // P: this wave's place in its pair (a compile-time value per branch, so that the chunks it owns
+            // are fixed registers).
+            auto body = [&](auto p_tag) {
+                constexpr int P = decltype(p_tag)::value;
+                if constexpr (WPP > 1) {
 #pragma unroll
-            for (int sl = 0; sl < NSL; ++sl) {
-                const int kr = 32 * sl + l32;
+                    for (int c = 0; c < NCK; ++c)
+                        if (c % 4 % WPP != P) *slot(wave, c) = chunk(c);
+                    barrier_lds();
+                }
 #pragma unroll
-                for (int dt = 0; dt < ND; ++dt)
+                for (int c = 0; c < NCK; ++c) {
+                    if (c % 4 % WPP != P) continue;
+                    f32x4 sum = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-                    for (int g = 0; g < 4; ++g) {
-                        const int cc = ((8 * dt + 2 * g + hh) ^ kr) & (CH4 - 1);
-                        *reinterpret_cast<f32x4*>(mine + kr * HD + 4 * cc) =
-                            f32x4{acc[sl][dt][4 * g], acc[sl][dt][4 * g + 1], acc[sl][dt][4 * g + 2], acc[sl][dt][4 * g + 3]};
-                    }
-            }
-            // LDS-only barriers: the loads and DMA of the next unit (K / V registers, A buffers) stay in
-            // flight; its loop waits for them (vmcnt) before reading either.
-            barrier_lds();
-            constexpr int KP = BNK * CH4 / 256;  // passes of the 256 threads over one pair's [64][HD] sums
-            static_assert(BNK * CH4 % 256 == 0, "whole passes per pair");
-#pragma unroll
-            for (int k = 0; k < PPB * KP; ++k) {
-                const int ps = k / KP;  // pair ps of the block: fixed per unrolled pass, so pbk stays scalar
-                const uint32_t rem = (uint32_t)etid + 256u * (k % KP);
-                const int row = rem / CH4, c = rem % CH4;
-                const int off = row * HD + 4 * ((c ^ row) & (CH4 - 1));
-                f32x4 sum = *reinterpret_cast<const f32x4*>(staged(ps * WPP) + off);
-#pragma unroll
-                for (int m = 1; m < WPP; ++m) sum += *reinterpret_cast<const f32x4*>(staged(ps * WPP + m) + off);
-                sum *= mul;
-                const int pbk = bgrp * PPB + ps;
-                if (pbk < BKV && kb0 + row < T) {
-                    if (nsplit == 1) {
-                        const int pb = pbk / KVH;
-                        u16* dst = out + lk.at(pb, pbk - pb * KVH) + (size_t)(kb0 + row) * lk.st + 4 * c;
-                        *reinterpret_cast<u32x2*>(dst) = u32x2{E::pack2(sum[0], sum[1]), E::pack2(sum[2], sum[3])};
-                    } else {  // this split's partial: part[split][dK | dV][bk][key][HD]
-                        float* dst = part + (((size_t)sidx * 2 + which) * BKV + pbk) * T * HD + (size_t)(kb0 + row) * HD + 4 * c;
-                        *reinterpret_cast<f32x4*>(dst) = sum;
+                    for (int m = 0; m < WPP; ++m) sum += m == P ? chunk(c) : *slot(wave - P + m, c);
+                    sum *= mul;
+                    const int key = kb0 + 32 * (c / (4 * ND)) + l32, col = 32 * (c / 4 % ND) + 8 * (c % 4) + 4 * hh;
+                    if (active && key < T) {
+                        if (nsplit == 1) {
+                            u16* dst = out + kvoff + (size_t)key * lk.st + col;
+                            *reinterpret_cast<u32x2*>(dst) = u32x2{E::pack2(sum[0], sum[1]), E::pack2(sum[2], sum[3])};
+                        } else {  // this split's partial: part[split][dK | dV][bk][key][HD]
+                            float* dst = part + (((size_t)sidx * 2 + which) * BKV + bk) * T * HD + (size_t)key * HD + col;
+                            *reinterpret_cast<f32x4*>(dst) = sum;
+                        }
                     }
                 }
+                if constexpr (WPP > 1) barrier_lds();  // the staging area is free again (for dV, then the next unit)
+            };
+            if constexpr (WPP == 1) {
+                body(std::integral_constant<int, 0>{});
+            } else {
+                const int pu = __builtin_amdgcn_readfirstlane(wp);
+                if (pu == 0) body(std::integral_constant<int, 0>{});
+                else if (WPP == 2 || pu == 1) body(std::integral_constant<int, 1>{});
+                else if constexpr (WPP == 4) {
+                    if (pu == 2) body(std::integral_constant<int, 2>{});
+                    else body(std::integral_constant<int, 3>{});
+                }
             }
-            barrier_lds();  // the staging area is free again (for dV, then for the next unit's B tiles)
         };
         reduce_store(dk, scale, dK, 0);
         reduce_store(dv, 1.f, dV, 1);
