@@ -790,20 +790,29 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(
             const int n1 = group * (nqt - un), i1 = first_of(n1);
             if (wp < end_of(n1) - i1) issue_it(i1 + wp, un, qA, oA, lA);
         }
-        if constexpr (WPP > 1) barrier_lds();  // every wave's loop is done: the B buffers can take the staged sums
         // Sum each pair's WPP partial dK^T, then dV^T, and store the sums. A wave's partial is NCK chunks of
-        // 1 KB: chunk (sl, dt, g) holds accumulator elements 4g .. 4g + 3 of acc[sl][dt] in every lane
+        // 1 KB: chunk c = (sl, dt, g) holds accumulator elements 4g .. 4g + 3 of acc[sl][dt] in every lane
         // (lane = key 32 sl + l32, element 4g + e = column 32 dt + 8g + 4hh + e). Chunk (sl, dt, g) belongs
-        // to wave g % WPP of the pair: the pair's other waves stage their copies of it in LDS (the B
-        // buffers, which the next unit's first tiles leave alone), and the owner adds them and its own in
-        // wave order and stores the sum. With one wave per pair nothing is staged and no wave waits for
-        // another. The LDS-only barriers leave the next unit's loads in flight.
+        // to wave g % WPP of the pair: the pair's other waves stage their copies of it in their LDS slots,
+        // and the owner adds them and its own in wave order. Each wave's slots are its own B tile slots,
+        // which only it used in its loop and the next unit's first tiles leave alone: a wave stages as soon
+        // as its loop is done, and with one wave per pair no wave waits for another. The LDS-only barriers
+        // leave the next unit's loads in flight.
+        // Without a split the owner rounds the sums to 16 bits and writes them back into its own slot of
+        // the chunk (dK in the first half, dV in the second: 32 rows of 16 bytes, row r at 16-byte group
+        // (r + j) % 32 with j = the chunk's 16-byte column group, so that the groups of one gradient row
+        // fall in different banks); then the pair's waves store whole gradient rows, 16 bytes per lane.
+        // With a split the owner stores its fp32 sums into the split's partial directly.
         constexpr int NCK = NSL * ND * 4;
-        static_assert(2 * NCK * 1024 <= NW * QT * 2, "two waves' staged chunks fit in one B tile buffer");
-        auto slot = [&](int w, int c) {  // wave w's staged copy of chunk c: waves 0, 1 in qB, waves 2, 3 in oB
-            return reinterpret_cast<f32x4*>(w < 2 ? qB : oB) + ((w & 1) * NCK + c) * 64 + lane;
+        constexpr int NG = HD / 8;  // 16-byte (8-column) groups per 16-bit gradient row
+        static_assert(NCK / 2 * 1024 == QT * 2, "a wave's chunks fill its two B tile slots");
+        auto slot = [&](int w, int c) {  // wave w's 1 KB slot for chunk c: half in its qB slot, half in oB
+            return reinterpret_cast<char*>((c < NCK / 2 ? qB : oB) + w * QT) + (c % (NCK / 2)) * 1024;
         };
-        auto reduce_store = [&](const f32x16 (&acc)[NSL][ND], float mul, u16* out, int which) {
+        auto row16 = [&](int w, int c, int which, int r) {  // 16-bit sums of row r (0..31) of chunk c
+            return reinterpret_cast<u32x4*>(slot(w, c) + which * 512) + ((r + c % (4 * ND)) & 31);
+        };
+        auto reduce = [&](const f32x16 (&acc)[NSL][ND], float mul, int which) {
             auto chunk = [&](int c) {
                 const f32x16& a = acc[c / (4 * ND)][c / 4 % ND];
                 const int g = c % 4;
@@ -816,7 +825,7 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(
                 if constexpr (WPP > 1) {
 #pragma unroll
                     for (int c = 0; c < NCK; ++c)
-                        if (c % 4 % WPP != P) *slot(wave, c) = chunk(c);
+                        if (c % 4 % WPP != P) reinterpret_cast<f32x4*>(slot(wave, c))[lane] = chunk(c);
                     barrier_lds();
                 }
 #pragma unroll
@@ -824,20 +833,21 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(
                     if (c % 4 % WPP != P) continue;
                     f32x4 sum = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-                    for (int m = 0; m < WPP; ++m) sum += m == P ? chunk(c) : *slot(wave - P + m, c);
+                    for (int m = 0; m < WPP; ++m)
+                        sum += m == P ? chunk(c) : reinterpret_cast<const f32x4*>(slot(wave - P + m, c))[lane];
                     sum *= mul;
-                    const int key = kb0 + 32 * (c / (4 * ND)) + l32, col = 32 * (c / 4 % ND) + 8 * (c % 4) + 4 * hh;
-                    if (active && key < T) {
-                        if (nsplit == 1) {
-                            u16* dst = out + kvoff + (size_t)key * lk.st + col;
-                            *reinterpret_cast<u32x2*>(dst) = u32x2{E::pack2(sum[0], sum[1]), E::pack2(sum[2], sum[3])};
-                        } else {  // this split's partial: part[split][dK | dV][bk][key][HD]
+                    if (nsplit == 1) {
+                        reinterpret_cast<u32x2*>(row16(wave, c, which, l32))[hh] =
+                            u32x2{E::pack2(sum[0], sum[1]), E::pack2(sum[2], sum[3])};
+                    } else {  // this split's partial: part[split][dK | dV][bk][key][HD]
+                        const int key = kb0 + 32 * (c / (4 * ND)) + l32, col = 32 * (c / 4 % ND) + 8 * (c % 4) + 4 * hh;
+                        if (active && key < T) {
                             float* dst = part + (((size_t)sidx * 2 + which) * BKV + bk) * T * HD + (size_t)key * HD + col;
                             *reinterpret_cast<f32x4*>(dst) = sum;
                         }
                     }
                 }
-                if constexpr (WPP > 1) barrier_lds();  // the staging area is free again (for dV, then the next unit)
+                if constexpr (WPP > 1) barrier_lds();  // staged copies read, 16-bit sums written
             };
             if constexpr (WPP == 1) {
                 body(std::integral_constant<int, 0>{});
@@ -851,8 +861,25 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(
                 }
             }
         };
-        reduce_store(dk, scale, dK, 0);
-        reduce_store(dv, 1.f, dV, 1);
+        reduce(dk, scale, 0);
+        reduce(dv, 1.f, 1);
+        if (nsplit == 1) {
+            // The pair's 64 x HD sums of each gradient: 64 NG groups of 16 bytes, 64 NG / WPP per wave.
+#pragma unroll
+            for (int k = 0; k < NG / WPP; ++k) {
+                const int G = (wp * (NG / WPP) + k) * 64 + lane;  // group G: row G / NG, column group G % NG
+                const int r = G / NG, j = G % NG;
+                const int c = r / 32 * 4 * ND + j;  // the chunk holding it, and its owner
+                const int ow = wave - wp + c % 4 % WPP;
+                const u32x4 vk = *row16(ow, c, 0, r & 31), vv = *row16(ow, c, 1, r & 31);
+                if (active && kb0 + r < T) {
+                    const size_t off = kvoff + (size_t)(kb0 + r) * lk.st + 8 * j;
+                    *reinterpret_cast<u32x4*>(dK + off) = vk;
+                    *reinterpret_cast<u32x4*>(dV + off) = vv;
+                }
+            }
+            if constexpr (WPP > 1) barrier_lds();  // the B buffers are free for the next unit
+        }
     }
 }
 
