@@ -637,9 +637,6 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(
         // Iteration itn -> 64-row query tile.
         auto qbase_of = [&](int itn) { return iter_tile(itn, qt_first) * BM; };
         auto issue = [&](int itn, u16* qs, u16* os, float* ls) { issue_it(itn, qt_first, qs, os, ls); };
-        // One 64-query iteration: two 32-query steps, each against both 32-key slabs.
-        // MASK: the iteration crosses the diagonal or T (a separate instantiation, so that unmasked
-        // iterations carry no per-element selects).
         // Operands of one 32-query step: Q / dO rows (A operands) and -lse/scale, -D as the
         // accumulators' initial values (element i: query 32qh + (i/4)*8 + 4hh + i%4, the same for
         // every key); and the Q^T / dO^T columns of its two 16-query chunks.
@@ -675,8 +672,8 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(
         };
         // One 64-query iteration: two 32-query steps, each against both 32-key slabs. The second
         // step's operands are read from LDS while the first step's products run.
-        // MASK: the iteration crosses the diagonal or T (a separate instantiation, so that unmasked
-        // iterations carry no per-element selects).
+        // MASK: the iteration crosses the diagonal (a separate instantiation, so that unmasked iterations
+        // carry no per-element selects).
         // DMA: the next iteration's tiles (iteration nitn into nqs / nos / nls) are copied during this
         // one, their copy instructions spread over the MFMAs (the CU's copy path accepts them only so
         // fast, and an in-order wave that issued them back to back would stall on it with its MFMA
@@ -713,24 +710,22 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(
                 }
 #pragma unroll
                 for (int sl = 0; sl < NSL; ++sl) {
+                    // Future keys (key > q) get the score -inf, so p = 0 and dS = 0. Keys past T (loaded as
+                    // key T - 1, and only in the last unit, whose one query tile is its diagonal) are future
+                    // keys of every row before T, and their columns are never stored. Rows past T start
+                    // from -inf (see below), so their p is 0 too.
+                    if constexpr (MASK) {
+                        const int key = kb0 + 32 * sl + l32;
+                        const int qlo = key - qbase - 32 * qh - 4 * hh;  // offsets below this: future
+#pragma unroll
+                        for (int i = 0; i < 16; ++i)
+                            s[sl][i] = (i >> 2) * 8 + (i & 3) >= qlo ? s[sl][i] : -INFINITY;
+                    }
 #pragma unroll
                     for (int i = 0; i < 16; ++i) {
                         const float p = fast_exp2(s[sl][i] * sl2);
                         dp[sl][i] *= p;
                         s[sl][i] = p;
-                    }
-                    if (MASK) {  // visible iff key <= q, q < T and key < T
-                        const int key = kb0 + 32 * sl + l32;
-                        const int qlo = key - qbase - 32 * qh - 4 * hh;  // offsets below this: future
-                        const int qhi = T - qbase - 32 * qh - 4 * hh;    // offsets at or above this: past T
-                        const bool kin = key < T;
-#pragma unroll
-                        for (int i = 0; i < 16; ++i) {
-                            const int qo = (i >> 2) * 8 + (i & 3);
-                            const bool keep = (qo >= qlo) & (qo < qhi) & kin;
-                            s[sl][i] = keep ? s[sl][i] : 0.f;
-                            dp[sl][i] = keep ? dp[sl][i] : 0.f;
-                        }
                     }
 #pragma unroll
                     for (int half = 0; half < 2; ++half) {
@@ -757,7 +752,11 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(
         auto run = [&](auto dma_tag, int itn, const u16* qs, const u16* os, const float* ls, int nitn, u16* nqs,
                        u16* nos, float* nls) {
             const int qbase = qbase_of(itn);
-            if ((kb0 + BNK - 1 > qbase) || (qbase + BM > T) || (kb0 + BNK > T))
+            // Rows past T (zero Q and dO rows; their -lse is row T - 1's, which with a zero score could
+            // overflow p) start their scores from -inf instead, so their p is 0: patched in this wave's
+            // copy of the -lse vector, which has landed.
+            if (qbase + BM > T && lane >= T - qbase) const_cast<float*>(ls)[wave * 2 * BM + lane] = -INFINITY;
+            if (kb0 + BNK - 1 > qbase)
                 compute(std::true_type{}, dma_tag, qbase, qs, os, ls, nitn, nqs, nos, nls);
             else
                 compute(std::false_type{}, dma_tag, qbase, qs, os, ls, nitn, nqs, nos, nls);
@@ -1024,9 +1023,9 @@ __global__ __launch_bounds__(256, 2) void fa_bwd_dq_kernel(const u16* __restrict
 #pragma unroll
         for (int t = 0; t < NT; ++t)
 #pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                const float ds = fast_exp2(fmaf(s[t][i], sl2, nl2)) * dp[t][i];
-                dp[t][i] = (MASK && 32 * t + (i >> 2) * 8 + (i & 3) > lim) ? 0.f : ds;
+            for (int i = 0; i < 16; ++i) {  // masked scores become -inf, so their dS is 0
+                const float sv = (MASK && 32 * t + (i >> 2) * 8 + (i & 3) > lim) ? -INFINITY : s[t][i];
+                dp[t][i] = fast_exp2(fmaf(sv, sl2, nl2)) * dp[t][i];
             }
 #pragma unroll
         for (int c = 0; c < BN / 16; ++c) {

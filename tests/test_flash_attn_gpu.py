@@ -167,6 +167,48 @@ def test_fewer_waves_per_unit_pair_matches_oracle(B, H, KVH, T, hd):
     _check(_run(q, k, v, do), _oracle(q, k, v, do), dtype, f"waves per pair {(B, H, KVH, T, hd)}")
 
 
+# A plain shape, an fp16 head_dim-32 MQA shape whose dK/dV work is split, and a bf16 split shape.
+SEPARATE = [(2, 12, 4, 300, 64, torch.bfloat16), (1, 12, 1, 700, 32, torch.float16), (2, 12, 1, 1024, 64, torch.bfloat16)]
+
+
+@pytest.mark.parametrize("B, H, KVH, T, hd, dtype", SEPARATE)
+def test_separate_backward_entry_points(B, H, KVH, T, hd, dtype):
+    """nn_fa_bwd_pre then nn_fa_bwd_dkdv, and nn_fa_bwd_dq, called on their own through the C ABI, give the
+    gradients of nn_fa_bwd (which runs nn_fa_bwd_dq's kernel, with the preprocessing fused, then dK/dV's).
+    dq is the same kernel on the same inputs: bit for bit. dk and dv match the oracle; against nn_fa_bwd's they
+    differ only in rounding, because the standalone pass sums D = rowsum(dO * o) in another order."""
+    from nanonemo_amd.kernels.hip import DTYPE_BF16, DTYPE_F16, check, lib
+
+    L = lib()
+    dt = DTYPE_BF16 if dtype == torch.bfloat16 else DTYPE_F16
+    print(f"\n[case] separate backward entry points B={B} H={H} KVH={KVH} T={T} hd={hd} {dtype}", flush=True)
+    qc, kc, vc, doc = make_inputs(B, H, KVH, T, hd, dtype, seed=5)
+    q, k, v, do = (t.to(DEV) for t in (qc, kc, vc, doc))
+    o, lse = torch.empty_like(q), torch.empty(B, H, T, device=DEV)
+    scale = 1.0 / math.sqrt(hd)
+    st = torch.cuda.current_stream().cuda_stream
+    p = lambda t: t.data_ptr()  # noqa: E731
+    check(L.nn_fa_fwd(p(q), p(k), p(v), p(o), p(lse), B, H, KVH, T, hd, dt, scale, st))
+    wsb = L.nn_fa_bwd_workspace_size(B, H, KVH, T, hd)
+    ws, ws2 = (torch.empty(wsb, dtype=torch.uint8, device=DEV) for _ in range(2))
+    dq, dq2 = torch.empty_like(q), torch.empty_like(q)
+    dk, dk2, dv, dv2 = torch.empty_like(k), torch.empty_like(k), torch.empty_like(v), torch.empty_like(v)
+    check(L.nn_fa_bwd(p(do), p(q), p(k), p(v), p(o), p(lse), p(dq), p(dk), p(dv), p(ws), wsb, B, H, KVH, T, hd,
+                      dt, scale, st))
+    check(L.nn_fa_bwd_pre(p(o), p(do), p(lse), p(ws2), wsb, B, H, KVH, T, hd, dt, scale, st))
+    check(L.nn_fa_bwd_dkdv(p(q), p(k), p(v), p(do), p(ws2), wsb, p(dk2), p(dv2), B, H, KVH, T, hd, dt, scale, st))
+    check(L.nn_fa_bwd_dq(p(q), p(k), p(v), p(o), p(do), p(lse), p(ws2), wsb, p(dq2), B, H, KVH, T, hd, dt, scale,
+                         st))
+    torch.cuda.synchronize()
+    assert torch.equal(dq2, dq)
+    ro, rlse = oracle.forward(*(t.double().numpy() for t in (qc, kc, vc)))
+    _, rdk, rdv = oracle.backward(*(t.double().numpy() for t in (doc, qc, kc, vc)), ro, rlse)
+    for name, x, x_fused, r in (("dk", dk2, dk, rdk), ("dv", dv2, dv, rdv)):
+        assert_close_tol(x.cpu(), torch.from_numpy(r), TOL_GRAD[dtype], f"separate {name}")
+        e = errors(x.double().cpu(), x_fused.double().cpu())
+        assert e["rel_fro"] <= 2e-3, f"separate {name} vs nn_fa_bwd: {e}"
+
+
 def test_deterministic_backward():
     # The backward has no atomics: the split dK/dV partials are summed in split order, the unsplit ones
     # through LDS in wave order, so repeated calls agree bit for bit.
