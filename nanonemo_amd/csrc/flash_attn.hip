@@ -749,13 +749,13 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(
                 }
             }
         };
-        auto run = [&](auto dma_tag, int itn, const u16* qs, const u16* os, const float* ls, int nitn, u16* nqs,
+        auto run = [&](auto dma_tag, int itn, const u16* qs, const u16* os, float* ls, int nitn, u16* nqs,
                        u16* nos, float* nls) {
             const int qbase = qbase_of(itn);
             // Rows past T (zero Q and dO rows; their -lse is row T - 1's, which with a zero score could
             // overflow p) start their scores from -inf instead, so their p is 0: patched in this wave's
             // copy of the -lse vector, which has landed.
-            if (qbase + BM > T && lane >= T - qbase) const_cast<float*>(ls)[wave * 2 * BM + lane] = -INFINITY;
+            if (qbase + BM > T && lane >= T - qbase) ls[wave * 2 * BM + lane] = -INFINITY;
             if (kb0 + BNK - 1 > qbase)
                 compute(std::true_type{}, dma_tag, qbase, qs, os, ls, nitn, nqs, nos, nls);
             else
