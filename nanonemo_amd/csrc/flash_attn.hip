@@ -5,15 +5,17 @@
 //
 //   * All products run on v_mfma_f32_32x32x16_{bf16,f16} with fp32 accumulators in VGPRs. One
 //     wave owns a 32-wide slab of the sequence dimension; LDS holds tiles shared by the block.
-//   * Tiles move global -> LDS with global_load_lds_dwordx4 (no staging registers) into
-//     row-major tiles whose 16-byte chunks are XOR-swizzled by row. Operands that need a
+//   * Tiles move global -> LDS with buffer_load_dwordx4 ... lds (no staging registers; the scalar
+//     buffer descriptor ends at row T - 1, so rows past it read as zeros) into row-major tiles
+//     whose 16-byte chunks are XOR-swizzled by row. Operands that need a
 //     row of a tile are read with ds_read_b128; operands that need a column (the transposed
 //     products) are read with ds_read_b64_tr_b16, so no transposed copy is ever stored.
 //   * Forward computes S^T = K Q^T so that each lane owns one query row (lane % 32) and the
 //     keys sit in its accumulator registers: the row max/sum are in-lane reductions plus one
 //     exchange with the other half-wave, and P^T feeds O^T += V^T P^T straight from registers.
-//     The running max is only moved when it grows by more than 2^8 (in base 2), so most tiles
-//     skip rescaling O; the row sum adds the 16-bit P that the product actually uses.
+//     The running max is only moved when a row's 16-bit p of one sub-tile sum past 2^28 (or one
+//     of them overflows the 16-bit format), so most tiles skip rescaling O; the row sum adds the
+//     16-bit P that the product actually uses.
 //   * Backward in two deterministic kernels with no atomics. dK/dV: keys outer; a block owns a
 //     64-key block, its waves walk the group's query heads x query tiles, S = Q K^T and
 //     dP = dO V^T land with the key on the lane, so P and dS feed dV^T += dO^T P and
@@ -68,8 +70,9 @@ constexpr int kBF16 = 1;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 // The forward keeps a stale running max m until a row's exponentials exp2(s - m) grow past this
-// bound (base-2 units): p <= 2^24 stays exact in the exponent range of fp32 and the 16-bit formats, and
-// a row's 16 values of a sub-tile then sum to at most 2^28.
+// bound (base-2 units): p <= 2^24 stays within the exponent range of fp32 and bf16, and a row's 16
+// values of a sub-tile then sum to at most 2^28. In fp16, whose largest value is 65504, a p that large
+// packs to inf, and that inf in the row sum triggers the rescale as well.
 constexpr float kGrowLog2 = 24.0f;
 constexpr float kPsumMax = 16.0f * 16777216.0f;  // 16 * 2^kGrowLog2
 
@@ -355,6 +358,9 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_kernel(const u16* __restrict__ 
         constexpr bool MASK = decltype(mask_tag)::value;
         const int lim = min(qrow, T - 1) - k0 - 4 * hh;  // key offsets beyond this are masked
         const int nt = MASK ? min(NT, (qw + 31 - k0) / 32 + 1) : NT;  // sub-tiles with a visible key
+        // The wave's smallest lim (lane 32: row qw, hh = 1): sub-tiles whose last key offset (32t + 27)
+        // does not exceed it are visible to every lane and skip the per-element selects.
+        const int lim_w = min(qw, T - 1) - k0 - 4;
         auto kops = [&](int t, u16x8* kq) {
 #pragma unroll
             for (int ks = 0; ks < NS; ++ks) kq[ks] = ld8(kb + 32 * t * HD + koff[ks]);
@@ -385,7 +391,7 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_kernel(const u16* __restrict__ 
                     va[half][dt] = cat4(ld_tr(vc + voff[dt][0]), ld_tr(vc + voff[dt][1]));
                 }
             // cur[i] = score of query qrow against key k0 + 32t + (i/4)*8 + 4hh + i%4.
-            if (MASK) {
+            if (MASK && 32 * t + 27 > lim_w) {
 #pragma unroll
                 for (int i = 0; i < 16; ++i) cur[i] = (32 * t + (i >> 2) * 8 + (i & 3) > lim) ? -INFINITY : cur[i];
             }
@@ -1020,13 +1026,18 @@ __global__ __launch_bounds__(256, 2) void fa_bwd_dq_kernel(const u16* __restrict
         }
         // s[t][i]: key k0 + 32t + (i/4)*8 + 4hh + i%4 against query qrow; dp[t][i] already holds dP - D.
         const int lim = min(qrow, T - 1) - k0 - 4 * hh;
+        // The wave's smallest lim (lane 32: row qw, hh = 1): sub-tiles whose last key offset (32t + 27)
+        // does not exceed it are visible to every lane and skip the per-element selects.
+        const int lim_w = min(qw, T - 1) - k0 - 4;
 #pragma unroll
-        for (int t = 0; t < NT; ++t)
+        for (int t = 0; t < NT; ++t) {
+            if (MASK && 32 * t + 27 > lim_w) {  // masked scores become -inf, so their dS is 0
 #pragma unroll
-            for (int i = 0; i < 16; ++i) {  // masked scores become -inf, so their dS is 0
-                const float sv = (MASK && 32 * t + (i >> 2) * 8 + (i & 3) > lim) ? -INFINITY : s[t][i];
-                dp[t][i] = fast_exp2(fmaf(sv, sl2, nl2)) * dp[t][i];
+                for (int i = 0; i < 16; ++i) s[t][i] = 32 * t + (i >> 2) * 8 + (i & 3) > lim ? -INFINITY : s[t][i];
             }
+#pragma unroll
+            for (int i = 0; i < 16; ++i) dp[t][i] = fast_exp2(fmaf(s[t][i], sl2, nl2)) * dp[t][i];
+        }
 #pragma unroll
         for (int c = 0; c < BN / 16; ++c) {
             const u16x8 sf = pack8<DT>(dp[c >> 1], 8 * (c & 1));  // keys 16c + (j/4)*8 + 4hh + j%4
