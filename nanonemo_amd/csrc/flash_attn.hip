@@ -699,9 +699,13 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(
             load_cols(0, qb_, ob_, c[0]);
 #pragma unroll
             for (int qh = 0; qh < 2; ++qh) {
+                // A masked iteration sits on the diagonal (its query tile is the unit: qbase == kb0), so
+                // slab sl against step qh is wholly future for sl > qh (no products at all: p = 0),
+                // wholly visible for sl < qh, and only sl == qh needs the per-element mask.
                 f32x16 s[NSL], dp[NSL];
 #pragma unroll
                 for (int sl = 0; sl < NSL; ++sl) {
+                    if (MASK && sl > qh) continue;
                     s[sl] = r[qh].s0;
                     dp[sl] = r[qh].d0;
 #pragma unroll
@@ -716,11 +720,12 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(
                 }
 #pragma unroll
                 for (int sl = 0; sl < NSL; ++sl) {
+                    if (MASK && sl > qh) continue;
                     // Future keys (key > q) get the score -inf, so p = 0 and dS = 0. Keys past T (loaded as
                     // key T - 1, and only in the last unit, whose one query tile is its diagonal) are future
                     // keys of every row before T, and their columns are never stored. Rows past T start
                     // from -inf (see below), so their p is 0 too.
-                    if constexpr (MASK) {
+                    if (MASK && sl == qh) {
                         const int key = kb0 + 32 * sl + l32;
                         const int qlo = key - qbase - 32 * qh - 4 * hh;  // offsets below this: future
 #pragma unroll
@@ -746,11 +751,12 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(
                     }
                 }
             }
-            if constexpr (DMA) {  // three MFMAs, then one copy instruction, kDmaOps times (denser stalls on
-                                  // the copy path, sparser leaves the last copies' latency exposed)
+            if constexpr (DMA) {  // three MFMAs (two in a masked iteration, which has 48), then one copy
+                                  // instruction, kDmaOps times (denser stalls on the copy path, sparser
+                                  // leaves the last copies' latency exposed)
 #pragma unroll
                 for (int k = 0; k < kDmaOps; ++k) {
-                    __builtin_amdgcn_sched_group_barrier(0x008, 3, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x008, MASK ? 2 : 3, 0);
                     __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
                 }
             }
