@@ -122,6 +122,22 @@ def test_extreme_score_range_matches_oracle(dtype):
     _check(got, _oracle(q, k, v, do), dtype, f"extreme x{mult:g} {dtype}")
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_rows_past_T_with_a_very_negative_last_lse(dtype):
+    # T % 64 != 0, so the last 64-row query tile has rows past T, and the last row's scores are all about
+    # -110 (natural-log units): keys are positive, and q[T-1] = -12. Its lse is then about -105, and a row
+    # past T that started its scores from that lse (zero Q) would get p = e^105, which overflows fp32. Such
+    # rows must contribute nothing: every output finite and on the float64 oracle.
+    B, H, KVH, T, hd = 1, 4, 2, 300, 64
+    q, k, v, do = make_inputs(B, H, KVH, T, hd, dtype, seed=7)
+    k = (k.float().abs() + 0.5).to(dtype)
+    q[:, :, T - 1, :] = -12.0
+    got = _run(q, k, v, do)
+    assert all(torch.isfinite(t).all() for t in got)
+    assert got[1][:, :, T - 1].max() < -100.0  # the case is the intended one
+    _check(got, _oracle(q, k, v, do), dtype, f"rows past T, very negative last lse {dtype}")
+
+
 def test_causal_future_keys_dont_leak():
     # Changing a key/value strictly after position i must not change output i (bit-exact).
     fa = _fa()
