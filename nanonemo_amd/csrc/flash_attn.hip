@@ -565,7 +565,9 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(
     const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
     const int wave = tid >> 6;  // a uniform copy in an SGPR costs this kernel more than it saves
     const int wp = wave % WPP;  // this wave's place among its pair's waves
-    const int bk = bgrp * PPB + wave / WPP;  // past BKV (the last block): the wave idles but keeps the barriers
+    // This wave's (batch, KV head); past BKV in the last block (the wave idles but keeps the barriers). With
+    // every wave on one pair it is the block's, a scalar, so the tile copies' addressing stays in SALU.
+    const int bk = WPP == NW ? bgrp : bgrp * PPB + wave / WPP;
     const bool active = bk < BKV;
     const int b = bk / KVH, kvh = bk - b * KVH, group = H / KVH;
     const DmaOffs<HD, BM, 1> dfo = dma_offsets<HD, BM, 1>(lane, 0, lq.st);
