@@ -19,8 +19,10 @@ from tests.common import make_inputs
 pytestmark = pytest.mark.gpu
 
 
-def _replays_match(launch, outs, n=4):
-    """Eager run, capture, then n poisoned replays compared bit for bit with the eager outputs."""
+def _replays_match(launch, outs, n=4, names=None):
+    """Eager run, capture, then n poisoned replays compared bit for bit with the eager outputs. A mismatch is
+    reported with the output it is in, how many elements differ, the largest difference and any NaNs."""
+    names = names or [f"output {i}" for i in range(len(outs))]
     launch(torch.cuda.current_stream().cuda_stream)
     torch.cuda.synchronize()
     ref = [t.clone() for t in outs]
@@ -41,8 +43,14 @@ def _replays_match(launch, outs, n=4):
         torch.cuda.synchronize()
         graph.replay()
         torch.cuda.synchronize()
-        for a, r in zip(outs, ref):
-            assert torch.equal(a, r), f"replay {i} differs from the eager result"
+        bad = []
+        for name, a, r in zip(names, outs, ref):
+            if not torch.equal(a, r):
+                d = (a.float() - r.float()).abs()
+                ne = (a != r).nonzero()
+                bad.append(f"{name}: {ne.shape[0]} of {a.numel()} elements differ, max |diff| {d.nan_to_num(float('inf')).max().item():.3e}, "
+                           f"NaNs in the replay {a.isnan().sum().item()}, first at {ne[0].tolist()}")
+        assert not bad, f"replay {i} differs from the eager result: " + "; ".join(bad)
         del junk
 
 
@@ -65,7 +73,7 @@ def test_captured_fwd_bwd_c_abi_calls_replay_bit_identically(B, H, KVH, T, D):
         check(L.nn_fa_bwd(p(do), p(q), p(k), p(v), p(o), p(lse), p(dq), p(dk), p(dv), p(ws), wsb, B, H, KVH, T, D,
                           DTYPE_BF16, 0.125, stream))
 
-    _replays_match(launch, [o, lse, dq, dk, dv])
+    _replays_match(launch, [o, lse, dq, dk, dv], names=["o", "lse", "dq", "dk", "dv"])
 
 
 def test_captured_rope_and_rmsnorm_c_abi_calls_replay_bit_identically():
