@@ -565,9 +565,11 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(
     const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
     const int wave = tid >> 6;  // a uniform copy in an SGPR costs this kernel more than it saves
     const int wp = wave % WPP;  // this wave's place among its pair's waves
-    // This wave's (batch, KV head); past BKV in the last block (the wave idles but keeps the barriers). With
-    // every wave on one pair it is the block's, a scalar, so the tile copies' addressing stays in SALU.
-    const int bk = WPP == NW ? bgrp : bgrp * PPB + wave / WPP;
+    // This wave's (batch, KV head); past BKV in the last block (the wave idles but keeps the barriers). It is
+    // wave-uniform and kept in a scalar register (with every wave on one pair it is the block's), so that the
+    // tile copies' addressing stays in SALU. (With one wave per pair the scalar form breaks the compiler's
+    // AGPR-copy rewrite pass.)
+    const int bk = WPP == NW ? bgrp : WPP == 2 ? __builtin_amdgcn_readfirstlane(bgrp * PPB + wave / WPP) : bgrp * PPB + wave / WPP;
     const bool active = bk < BKV;
     const int b = bk / KVH, kvh = bk - b * KVH, group = H / KVH;
     const DmaOffs<HD, BM, 1> dfo = dma_offsets<HD, BM, 1>(lane, 0, lq.st);
