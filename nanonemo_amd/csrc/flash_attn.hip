@@ -612,9 +612,10 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(
         // Wave-uniform in fact; made uniform for the compiler only here, so that the tile addressing is
         // scalar without keeping scalar copies alive across the whole kernel.
         const int itu = __builtin_amdgcn_readfirstlane(itn), wu = __builtin_amdgcn_readfirstlane(wave);
-        const int hq = kvh * group + iter_head(itu, qtf);
-        const size_t ro = ((size_t)b * H + hq) * T;  // first row of the head's [T] vectors
-        const size_t qo = lq.at(b, hq);
+        const int bu = __builtin_amdgcn_readfirstlane(b), ku = __builtin_amdgcn_readfirstlane(kvh);
+        const int hq = ku * group + iter_head(itu, qtf);
+        const size_t ro = ((size_t)bu * H + hq) * T;  // first row of the head's [T] vectors
+        const size_t qo = lq.at(bu, hq);
         const int q0 = iter_tile(itu, qtf) * BM;
         dma_rows<HD, BM, 1>(Q + qo, lq.st, q0, T, qs + wu * QT, 0, dfo);
         dma_rows<HD, BM, 1>(dO + qo, lq.st, q0, T, os + wu * QT, 0, dfo);
