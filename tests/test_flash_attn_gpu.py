@@ -109,6 +109,45 @@ def test_edge_shapes(B, H, KVH, T, hd):
     _check(_run(q, k, v, do), _oracle(q, k, v, do), dtype, f"edge {(B, H, KVH, T, hd)}")
 
 
+def _random_shapes(n, seed=2024):
+    """n seeded (B, H, KVH, T, hd, dtype) draws: T in 1..400, every divisor of H as KVH, both head dims."""
+    import random
+
+    rng = random.Random(seed)
+    out = []
+    for i in range(n):
+        H = rng.choice([1, 2, 3, 4, 6, 8, 12, 16])
+        KVH = rng.choice([d for d in range(1, H + 1) if H % d == 0])
+        out.append((rng.choice([1, 2]), H, KVH, rng.randint(1, 400), rng.choice([32, 64]),
+                    (torch.bfloat16, torch.float16)[i % 2]))
+    return out
+
+
+@pytest.mark.parametrize("B, H, KVH, T, hd, dtype", _random_shapes(16))
+def test_random_shapes_match_oracle(B, H, KVH, T, hd, dtype):
+    q, k, v, do = make_inputs(B, H, KVH, T, hd, dtype, seed=1000 + T)
+    _check(_run(q, k, v, do), _oracle(q, k, v, do), dtype, f"random {(B, H, KVH, T, hd, dtype)}")
+
+
+@pytest.mark.parametrize("B, T", [(0, 64), (2, 0)])
+def test_empty_problem_through_the_ops(B, T):
+    """No batch or no rows: both layouts' forward and backward return empty results of the right shapes."""
+    fa = _fa()
+    q = torch.randn(B, 12, T, 64, device=DEV).to(torch.bfloat16).requires_grad_()
+    k = torch.randn(B, 4, T, 64, device=DEV).to(torch.bfloat16).requires_grad_()
+    v = torch.randn(B, 4, T, 64, device=DEV).to(torch.bfloat16).requires_grad_()
+    o, lse = fa._flash_attn(q, k, v)
+    assert o.shape == q.shape and lse.shape == (B, 12, T) and lse.dtype == torch.float32
+    dq, dk, dv = torch.autograd.grad(o, (q, k, v), torch.ones_like(o))
+    assert dq.shape == q.shape and dk.shape == k.shape and dv.shape == v.shape
+    qt, kt, vt = (t.detach().transpose(1, 2).contiguous().requires_grad_() for t in (q, k, v))
+    ot = fa.flash_attn_bthd(qt, kt, vt)
+    assert ot.shape == qt.shape
+    grads = torch.autograd.grad(ot, (qt, kt, vt), torch.ones_like(ot))
+    assert [g.shape for g in grads] == [qt.shape, kt.shape, vt.shape]
+    torch.cuda.synchronize()
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 def test_extreme_score_range_matches_oracle(dtype):
     # Inputs x12: scores with standard deviation ~144, so a row's running max jumps by hundreds (base 2)
