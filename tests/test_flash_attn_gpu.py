@@ -129,6 +129,40 @@ def test_random_shapes_match_oracle(B, H, KVH, T, hd, dtype):
     _check(_run(q, k, v, do), _oracle(q, k, v, do), dtype, f"random {(B, H, KVH, T, hd, dtype)}")
 
 
+def test_long_sequence_prefix_and_zero_tail():
+    """T=65536 (B=1, 12 Q / 4 KV heads, d=64, bf16), checked through properties that hold at any length.
+
+    * Causal prefix: o, lse and dq of the first P rows depend only on rows and keys < P, so they are bit-identical
+      to a run on the P-row prefix.
+    * dO is zero past row P, so every dS of those rows is 0. dK/dV of keys < P then match the prefix run's, up to the
+      order of their fp32 sums (the two shapes split the work differently), and dK/dV of keys >= P are exactly 0.
+    * Each output row is a convex combination of V rows, so it stays within V's range.
+    """
+    torch.manual_seed(7)
+    B, H, KVH, T, hd, P = 1, 12, 4, 65536, 64, 1024
+    dt = torch.bfloat16
+    q = torch.randn(B, H, T, hd, device=DEV).to(dt)
+    k = torch.randn(B, KVH, T, hd, device=DEV).to(dt)
+    v = torch.randn(B, KVH, T, hd, device=DEV).to(dt)
+    do = torch.randn(B, H, T, hd, device=DEV).to(dt)
+    do[:, :, P:] = 0
+    fa = _fa()
+    o, lse = fa._flash_attn(q, k, v)
+    dq, dk, dv = fa._flash_attn_bwd(do, q, k, v, o, lse)
+    qp, kp, vp, dop = (t[:, :, :P].contiguous() for t in (q, k, v, do))
+    op_, lsep = fa._flash_attn(qp, kp, vp)
+    dqp, dkp, dvp = fa._flash_attn_bwd(dop, qp, kp, vp, op_, lsep)
+    torch.cuda.synchronize()
+    assert torch.equal(o[:, :, :P], op_) and torch.equal(lse[:, :, :P], lsep)
+    assert torch.equal(dq[:, :, :P], dqp)
+    assert not dq[:, :, P:].any() and not dk[:, :, P:].any() and not dv[:, :, P:].any()
+    assert_close_tol(dk[:, :, :P], dkp, TOL_GRAD[dt], "dk prefix")
+    assert_close_tol(dv[:, :, :P], dvp, TOL_GRAD[dt], "dv prefix")
+    assert torch.isfinite(lse).all() and torch.isfinite(o).all()
+    vmax = v.float().abs().amax(dim=(0, 2)).repeat_interleave(H // KVH, dim=0)  # [H, hd]
+    assert (o.float().abs() <= vmax[None, :, None, :] * (1 + 2 ** -7) + 1e-6).all()
+
+
 @pytest.mark.parametrize("B, T", [(0, 64), (2, 0)])
 def test_empty_problem_through_the_ops(B, T):
     """No batch or no rows: both layouts' forward and backward return empty results of the right shapes."""
