@@ -52,8 +52,9 @@ int nn_fa_fwd_strided(const void* q, const void* k, const void* v, void* o, floa
 /* Bytes of device workspace the backward needs: -rowsum(dO * o) and -lse / scale, one fp32 each
  * per query row, and, for shapes whose B * KVH * ceil(T / 128) dK/dV work units are too few to fill
  * the chip (under 256), split partials of dk and dv: S * 2 * B * KVH * T * D fp32 with
- * S = min(16, ceil(256 / units)). The caller allocates it, 256-byte aligned; its contents on entry
- * do not matter. */
+ * S = min(16, ceil(256 / units), (H / KVH) * (ceil(T / 64) + 1) / 8) and S >= 1 (every split keeps
+ * at least 8 of a unit pair's iterations), or S = 1 when (H / KVH) * ceil(T / 64) * 16 reaches 2^31.
+ * The caller allocates the size returned here, 256-byte aligned; its contents on entry do not matter. */
 size_t nn_fa_bwd_workspace_size(int64_t B, int64_t H, int64_t KVH, int64_t T, int64_t D);
 
 /* Backward: (dq, dk, dv) in the input dtype, contiguous. dk/dv hold the sum over the
