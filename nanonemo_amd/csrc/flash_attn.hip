@@ -240,6 +240,28 @@ __device__ inline void dma_rows(const u16* __restrict__ g, int ld, int r0, int T
 #endif
 }
 
+// Block -> (batch * H + head, query block) for the forward and dQ grids of nqb * BH blocks: heaviest
+// query blocks first (the causal work of a block grows with its index). Blocks are dispatched to the
+// 8 XCDs round-robin (block i to XCD i % 8), and each XCD has its own L2. When the B * KVH head groups
+// divide evenly over the XCDs, the blocks of every query head of one group go to the same XCD
+// (group g to XCD g % 8, heaviest first within the XCD), so that the group's K / V tiles are fetched
+// into one L2 instead of H / KVH of them. Otherwise blocks of one (batch, head) still share an XCD
+// when BH % 8 == 0.
+struct QBlk {
+    int bh, qb;
+};
+__device__ inline QBlk qblock_of(int bid, int BH, int group, int nqb) {
+    const int G = BH / group;  // (batch, KV head) groups
+    if (G % 8 == 0) {
+        const int x = bid & 7, slot = bid >> 3;
+        const int per = (G >> 3) * group;  // blocks of one query-block index on one XCD
+        const int qi = slot / per, r = slot - qi * per;
+        const int gi = r / group, hq = r - gi * group;
+        return {(gi * 8 + x) * group + hq, nqb - 1 - qi};
+    }
+    return {bid % BH, nqb - 1 - bid / BH};
+}
+
 // Element strides of a [B][heads][T][D] tensor view whose D stride is 1: batch, head and row
 // (sequence position). Q, O, dO and dQ share one layout; K, V, dK and dV another.
 struct Lay {
@@ -302,10 +324,8 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_kernel(const u16* __restrict__ 
     __shared__ __attribute__((aligned(16))) u16 kB[TILE];
     __shared__ __attribute__((aligned(16))) u16 vB[TILE];
 
-    // Heaviest query blocks first; blocks of one (batch, head) share an XCD when BH % 8 == 0.
-    const int bid = blockIdx.x;
-    const int bh = bid % BH;
-    const int qb = nqb - 1 - bid / BH;
+    const QBlk blk = qblock_of(blockIdx.x, BH, H / KVH, nqb);
+    const int bh = blk.bh, qb = blk.qb;
     const int b = bh / H, h = bh - b * H;
     const int kvh = h / (H / KVH);
     const size_t qoff = lq.at(b, h);
@@ -953,9 +973,8 @@ __global__ __launch_bounds__(256, 2) void fa_bwd_dq_kernel(const u16* __restrict
     __shared__ __attribute__((aligned(16))) u16 kB[TILE];
     __shared__ __attribute__((aligned(16))) u16 vB[TILE];
 
-    const int bid = blockIdx.x;
-    const int bh = bid % BH;
-    const int qb = nqb - 1 - bid / BH;
+    const QBlk blk = qblock_of(blockIdx.x, BH, H / KVH, nqb);
+    const int bh = blk.bh, qb = blk.qb;
     const int b = bh / H, h = bh - b * H;
     const int kvh = h / (H / KVH);
     const size_t qoff = lq.at(b, h);

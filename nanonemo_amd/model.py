@@ -104,9 +104,12 @@ class AddRMSNorm(RMSNorm):
 
 
 def rope_tables(head_dim: int, max_seq_len: int, base: float) -> tuple[torch.Tensor, torch.Tensor]:
-    """cos, sin of m * theta_i, shape (max_seq_len, head_dim // 2), fp32 (layers.py:59-64)."""
-    inv_freq = base ** (-torch.arange(0, head_dim, 2, dtype=torch.float32) / head_dim)
-    ang = torch.arange(max_seq_len, dtype=torch.float32)[:, None] * inv_freq[None, :]
+    """cos, sin of m * theta_i, shape (max_seq_len, head_dim // 2), fp32 (layers.py:59-64).
+
+    theta_i = 1 / base^(2i / head_dim), rounded as the reference rounds it (a reciprocal of the fp32 power,
+    not a negative power: the two differ in the last bit for some i), and m * theta_i as one fp32 product."""
+    inv_freq = 1.0 / (base ** (torch.arange(0, head_dim, 2, dtype=torch.float32) / head_dim))
+    ang = torch.outer(torch.arange(max_seq_len, dtype=torch.float32), inv_freq)
     return ang.cos(), ang.sin()
 
 

@@ -51,6 +51,21 @@ def test_rope_is_the_same_in_both_layouts():
     assert torch.equal(a, b)
 
 
+def test_rope_tables_are_bit_identical_to_the_reference_formula():
+    # The reference's rope_cache (/root/reference/nanonemo/model/layers.py:59-64): inv_freq as the reciprocal
+    # of an fp32 power, angles as torch.outer of fp32 positions and inv_freq. base**(-x) differs from
+    # 1/(base**x) in the last bit for some i, which moves thousands of cos/sin entries at T=1024.
+    for hd, T, base in ((64, 1024, 10000.0), (32, 300, 10000.0), (64, 64, 500000.0)):
+        inv = 1.0 / (base ** (torch.arange(0, hd, 2, dtype=torch.float32) / hd))
+        ang = torch.outer(torch.arange(T, dtype=torch.float32), inv)
+        cos, sin = rope_tables(hd, T, base)
+        assert cos.dtype == sin.dtype == torch.float32 and cos.shape == (T, hd // 2)
+        assert torch.equal(cos, ang.cos()) and torch.equal(sin, ang.sin()), (hd, T, base)
+    # and the negative-power form is not the same table (so the check above can tell them apart)
+    neg = 10000.0 ** (-torch.arange(0, 64, 2, dtype=torch.float32) / 64)
+    assert not torch.equal(torch.outer(torch.arange(1024, dtype=torch.float32), neg).cos(), rope_tables(64, 1024, 10000.0)[0])
+
+
 def test_rope_closed_forms():
     cos, sin = rope_tables(8, 16, 10000.0)
     x = torch.randn(1, 1, 16, 8, dtype=torch.float64).float()

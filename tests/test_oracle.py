@@ -227,3 +227,54 @@ def test_golden_fixture_reproduces(name):
     dq, dk, dv = A.backward(dod, qd, kd, vd, o, lse)
     for key, x in (("o", o), ("lse", lse), ("dq", dq), ("dk", dk), ("dv", dv)):
         np.testing.assert_allclose(x, g[key].numpy(), rtol=1e-6, atol=1e-6, err_msg=key)
+
+
+# ---- the timed CPU baseline (torch_reference_fwd_bwd), both forms ------------------------------
+
+
+def _check_torch_reference_fn(shape, explicit, seed=12):
+    """torch_reference_fwd_bwd in float64 against the pinned forward / backward at 1e-10."""
+    q, k, v, do = _rand(*shape, seed=seed)
+    o, lse = A.forward(q, k, v)
+    dq, dk, dv = A.backward(do, q, k, v, o, lse)
+    got = A.torch_reference_fwd_bwd(*(torch.tensor(x, dtype=torch.float64) for x in (q, k, v, do)), explicit=explicit)
+    for name, x, r in zip(("o", "dq", "dk", "dv"), got, (o, dq, dk, dv)):
+        assert x.dtype == torch.float64, name
+        np.testing.assert_allclose(x.numpy(), r, rtol=1e-10, atol=1e-10, err_msg=f"{name} explicit={explicit}")
+
+
+@pytest.mark.parametrize("explicit", [False, True])
+@pytest.mark.parametrize("shape", [(1, 12, 4, 40, 64), (2, 6, 2, 17, 32), (1, 4, 1, 9, 16), (1, 3, 3, 5, 8)])
+def test_torch_reference_fwd_bwd_matches_pinned_oracle(shape, explicit):
+    _check_torch_reference_fn(shape, explicit)
+
+
+def test_torch_reference_fwd_bwd_config1_shape():
+    # BASELINE config 1 (B=1, T=256, 12 Q / 4 KV heads, d=64), the shape the CPU baseline times.
+    _check_torch_reference_fn((1, 12, 4, 256, 64), explicit=False, seed=0)
+    _check_torch_reference_fn((1, 12, 4, 256, 64), explicit=True, seed=0)
+
+
+@pytest.mark.parametrize("explicit", [False, True])
+def test_planted_repeat_instead_of_repeat_interleave_is_caught(monkeypatch, explicit):
+    # K/V tiled [kv0, kv1, kv0, kv1, ...] instead of [kv0, kv0, ..., kv1, ...]: the wrong GQA grouping.
+    def tiled(self, repeats, dim=None, **kw):
+        reps = [1] * self.dim()
+        reps[dim] = repeats
+        return self.repeat(*reps)
+
+    monkeypatch.setattr(torch.Tensor, "repeat_interleave", tiled)
+    assert _fails(lambda: _check_torch_reference_fn((1, 12, 4, 24, 32), explicit))
+
+
+def test_planted_dropped_is_causal_is_caught(monkeypatch):
+    sdpa = F.scaled_dot_product_attention
+    monkeypatch.setattr(F, "scaled_dot_product_attention", lambda *a, is_causal=False, **kw: sdpa(*a, **kw))
+    assert _fails(lambda: _check_torch_reference_fn((1, 4, 2, 24, 32), explicit=False))
+
+
+def test_planted_wrong_explicit_mask_diagonal_is_caught(monkeypatch):
+    triu = torch.triu
+    monkeypatch.setattr(torch, "triu", lambda x, diagonal=0: triu(x, diagonal + 1))
+    assert _fails(lambda: _check_torch_reference_fn((1, 4, 2, 24, 32), explicit=True))
+
