@@ -106,6 +106,19 @@ int nn_fa_bwd_dq(const void* q, const void* k, const void* v, const void* o, con
                  int64_t B, int64_t H, int64_t KVH, int64_t T, int64_t D,
                  int dtype, float scale, void* stream);
 
+/* Backward that allocates nothing: as nn_fa_bwd, with the workspace taken from a 32 MiB device array
+ * inside the library (one per GPU, held until the process ends) instead of a caller buffer. No
+ * counterpart in the reference: it is for callers that cannot allocate (code under HIP-graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc). Shapes whose nn_fa_bwd_workspace_size exceeds
+ * 32 MiB (33554432 bytes; e.g. B * H * T above 4M query rows) are rejected with an error. The current
+ * device must own `stream`; the first call on a device looks the array up (hipGetSymbolAddress), no call
+ * allocates or frees. Calls that overlap on one GPU (other streams or threads) share the array and race;
+ * calls in one stream's order do not. */
+int nn_fa_bwd_noalloc(const void* dO, const void* q, const void* k, const void* v, const void* o,
+                      const float* lse, void* dq, void* dk, void* dv,
+                      int64_t B, int64_t H, int64_t KVH, int64_t T, int64_t D,
+                      int dtype, float scale, void* stream);
+
 /* Message of the last failed call on this thread ("" if none). Replaces the TORCH_CHECK
  * messages of flash_attn.cu:342-356 and :383-385. */
 const char* nn_fa_last_error(void);

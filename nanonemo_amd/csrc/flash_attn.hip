@@ -43,6 +43,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <mutex>
 #include <string>
 #include <type_traits>
 
@@ -1298,7 +1299,7 @@ int check_ws(void* workspace, size_t workspace_bytes, int64_t B, int64_t H, int6
 
 NNFA_API const char* nn_fa_last_error(void) { return g_last_error.c_str(); }
 
-NNFA_API int nn_fa_abi_version(void) { return 7; }
+NNFA_API int nn_fa_abi_version(void) { return 8; }
 
 NNFA_API size_t nn_fa_bwd_workspace_size(int64_t B, int64_t H, int64_t KVH, int64_t T, int64_t D) {
     if (B < 0 || H < 0 || KVH < 0 || T < 0 || D < 0) return 0;
@@ -1453,4 +1454,66 @@ NNFA_API int nn_fa_bwd_strided(const void* dO, const void* q, const void* k, con
     if (!qo_strides || !kv_strides) return fail(-1, "null strides");
     return bwd_entry(dO, q, k, v, o, lse, dq, dk, dv, workspace, workspace_bytes, B, H, KVH, T, D, dtype, scale,
                      qo_strides, kv_strides, stream);
+}
+
+// ------------------------------------------------------------------------------------------
+// Backward with no allocation at all: the workspace of nn_fa_bwd (-D, -lse/scale and, for split shapes,
+// the dK/dV partials) lives in this file-scope device array instead of a caller buffer. Each GPU the
+// library runs on holds its own copy for the life of the process. Every call on one GPU uses that GPU's
+// copy, so calls that overlap on one GPU (concurrent streams, or threads) race on it; calls in stream
+// order do not. Nothing in it needs to start at zero: the dQ kernel writes every -D / -lse/scale entry
+// before the dK/dV kernel reads it, and every split partial is written before the sum kernel reads it.
+// ------------------------------------------------------------------------------------------
+constexpr size_t kNoAllocScratchBytes = (size_t)32 << 20;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices];  // device address of `scratch` on each device, looked up once per device
+
+// The device address of `scratch` on the current device (which must own `stream`). In host code the
+// array's name is only a host-side handle; hipGetSymbolAddress, with the device current, gives that
+// device's copy. Looked up on the first call on each device and kept.
+int scratch_ptr(void* stream, void** out) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return fail((int)e, "hipGetDevice failed: %s", hipGetErrorString(e));
+    if (dev < 0 || dev >= kMaxDevices) return fail(-1, "device %d is out of the supported range", dev);
+    if (stream) {
+        int sdev = -1;
+        e = hipStreamGetDevice((hipStream_t)stream, &sdev);
+        if (e != hipSuccess) return fail((int)e, "hipStreamGetDevice failed: %s", hipGetErrorString(e));
+        if (sdev != dev) return fail(-1, "the stream belongs to device %d but device %d is current", sdev, dev);
+    }
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p)
+            return fail(e != hipSuccess ? (int)e : -1, "hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
+                        hipGetErrorString(e));
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return 0;
+}
+
+}  // namespace
+
+NNFA_API int nn_fa_bwd_noalloc(const void* dO, const void* q, const void* k, const void* v, const void* o,
+                               const float* lse, void* dq, void* dk, void* dv, int64_t B, int64_t H, int64_t KVH,
+                               int64_t T, int64_t D, int dtype, float scale, void* stream) {
+    g_last_error.clear();
+    if (int e = check_dims(B, H, KVH, T, D, dtype)) return e;
+    if (B == 0 || T == 0) return 0;
+    const size_t need = carve(nullptr, B, H, KVH, T, D).bytes;
+    if (need > kNoAllocScratchBytes)
+        return fail(-1, "nn_fa_bwd_noalloc: this shape needs %zu bytes of workspace, more than the %zu-byte scratch; "
+                    "use nn_fa_bwd with a caller workspace", need, kNoAllocScratchBytes);
+    void* ws = nullptr;
+    if (int e = scratch_ptr(stream, &ws)) return e;
+    return bwd_entry(dO, q, k, v, o, lse, dq, dk, dv, ws, kNoAllocScratchBytes, B, H, KVH, T, D, dtype, scale, nullptr,
+                     nullptr, stream);
 }

@@ -50,6 +50,9 @@ SIGNATURES: dict[str, tuple] = {
     "nn_fa_bwd_dq": (
         _int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp, _i64, _i64, _i64, _i64, _i64, _int, _f32, _vp]
     ),
+    "nn_fa_bwd_noalloc": (
+        _int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _int, _f32, _vp]
+    ),
     "nn_fa_last_error": (ctypes.c_char_p, []),
     "nn_fa_abi_version": (_int, []),
     # include/nanonemo_rope.h
@@ -71,7 +74,7 @@ SIGNATURES: dict[str, tuple] = {
     "nn_rmsnorm_last_error": (ctypes.c_char_p, []),
 }
 
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 
 @cache

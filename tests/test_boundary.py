@@ -303,3 +303,15 @@ def test_product_never_imports_the_oracle():
             text = path.read_text()
             assert not re.search(r"^\s*(from|import)\s+oracle\b", text, re.M), path
             assert "oracle/" not in text, path
+
+
+def test_noalloc_backward_checks_shape_before_touching_the_device():
+    # The argument checks of nn_fa_bwd_noalloc run before any HIP call: an empty problem is a no-op and a shape
+    # whose workspace exceeds the library's 32 MiB array is rejected with a message, here without a GPU.
+    L = lib()
+    assert L.nn_fa_bwd_noalloc(*([None] * 9), 0, 12, 4, 1024, 64, 1, 0.125, None) == 0
+    B, H, KVH, T, D = 64, 16, 4, 8192, 64
+    assert L.nn_fa_bwd_workspace_size(B, H, KVH, T, D) > 32 << 20
+    assert L.nn_fa_bwd_noalloc(*([None] * 9), B, H, KVH, T, D, 1, 0.125, None) == -1
+    assert b"32 MiB" in L.nn_fa_last_error() or b"scratch" in L.nn_fa_last_error()
+    assert L.nn_fa_bwd_noalloc(*([None] * 9), 1, 12, 5, 64, 64, 1, 0.125, None) == -1  # 12 % 5 != 0

@@ -1,0 +1,60 @@
+"""nn_fa_bwd_noalloc (the backward whose workspace is the library's own device array) against nn_fa_bwd with a
+caller workspace, through the C ABI: bit-identical outputs (the same kernels on the same inputs), on two calls
+in a row where the second is smaller (the array keeps the first call's contents), at an unsplit shape and at a
+shape whose dK/dV work is split (partials in the array), and a shape too large for the array is rejected."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from tests.common import make_inputs
+
+pytestmark = pytest.mark.gpu
+
+
+def _run_both(L, B, H, KVH, T, D, seed):
+    from nanonemo_amd.kernels.hip import DTYPE_BF16, check
+
+    print(f"\n[case] nn_fa_bwd_noalloc vs nn_fa_bwd B={B} H={H} KVH={KVH} T={T} D={D} seed={seed}", flush=True)
+    q, k, v, do = (t.cuda() for t in make_inputs(B, H, KVH, T, D, torch.bfloat16, seed=seed))
+    o, lse = torch.empty_like(q), torch.empty(B, H, T, device="cuda")
+    sp = torch.cuda.current_stream().cuda_stream
+    p = lambda t: t.data_ptr()  # noqa: E731
+    check(L.nn_fa_fwd(p(q), p(k), p(v), p(o), p(lse), B, H, KVH, T, D, DTYPE_BF16, D ** -0.5, sp))
+    wsb = L.nn_fa_bwd_workspace_size(B, H, KVH, T, D)
+    ws = torch.empty(wsb, dtype=torch.uint8, device="cuda")
+    ref = [torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)]
+    check(L.nn_fa_bwd(p(do), p(q), p(k), p(v), p(o), p(lse), *(p(t) for t in ref), p(ws), wsb, B, H, KVH, T, D,
+                      DTYPE_BF16, D ** -0.5, sp))
+    got = [torch.full_like(t, float("nan")) for t in ref]
+    check(L.nn_fa_bwd_noalloc(p(do), p(q), p(k), p(v), p(o), p(lse), *(p(t) for t in got), B, H, KVH, T, D,
+                              DTYPE_BF16, D ** -0.5, sp))
+    torch.cuda.synchronize()
+    for name, a, r in zip(("dq", "dk", "dv"), got, ref):
+        assert torch.equal(a, r), f"{name} differs at B={B} H={H} KVH={KVH} T={T}: max |diff| {(a.float() - r.float()).abs().max().item()}"
+
+
+@pytest.mark.parametrize(
+    "first, second",
+    [
+        ((8, 12, 4, 1024, 64), (2, 12, 4, 200, 64)),  # unsplit, then a smaller ragged one
+        ((2, 12, 1, 1024, 64), (1, 12, 1, 300, 32)),  # split dK/dV (partials in the array), then smaller
+    ],
+)
+def test_noalloc_backward_matches_workspace_backward_twice(first, second):
+    from nanonemo_amd.kernels.hip import lib
+
+    L = lib()
+    _run_both(L, *first, seed=5)
+    _run_both(L, *second, seed=6)
+
+
+def test_noalloc_backward_rejects_shapes_beyond_its_array():
+    from nanonemo_amd.kernels.hip import DTYPE_BF16, lib
+
+    L = lib()
+    B, H, KVH, T, D = 64, 16, 4, 8192, 64  # -D and -lse/scale alone need 64 MiB
+    assert L.nn_fa_bwd_workspace_size(B, H, KVH, T, D) > 32 << 20
+    rc = L.nn_fa_bwd_noalloc(*([None] * 9), B, H, KVH, T, D, DTYPE_BF16, 0.125, torch.cuda.current_stream().cuda_stream)
+    assert rc != 0 and b"scratch" in L.nn_fa_last_error()
