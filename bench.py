@@ -3,25 +3,29 @@
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--dtype bf16|fp16] [--batch 8] [--seq 1024]
     python bench.py --sweep        # step and per-kernel times over the SWEEP shapes, one JSON line each
 
-A step is one forward + backward of the hot path through the drop-in C ABI (nn_fa_fwd then nn_fa_bwd,
-include/nanonemo_fa.h) on synthetic N(0,1) inputs already resident in HBM, with outputs and the backward
-workspace allocated once. The same step captured once into a HIP graph and replayed K times is reported as
-graph_ms_per_step (the reference benchmark's method, without its cache flush). Default workload: B=8, T=1024, 12 query / 4 KV heads, head_dim 64, bf16 (the
-north-star shape of BASELINE.json). W untimed steps, then K timed steps between device
-synchronisations. The same pair through the torch.library ops (nanonemo::flash_attn +
-nanonemo::flash_attn_bwd, which add output allocation and Python dispatch) is timed beside it as
-op_ms_per_step.
+A step is one forward + backward of the hot path through the drop-in torch.library ops (nanonemo::flash_attn
+then nanonemo::flash_attn_bwd, which call the C ABI of include/nanonemo_fa.h) on synthetic N(0,1) inputs
+resident in HBM. Default workload: B=8, T=1024, 12 query / 4 KV heads, head_dim 64, bf16 (the north-star shape
+of BASELINE.json). W untimed warmup steps, about 1 s of settling steps, then K timed steps between device
+synchronisations. Each timed step follows a 512 MiB cache-flush write (twice the Infinity Cache, the reference
+benchmark's method, benchmarks/kernels/common.py:30-54) and is timed alone with HIP events on the launch
+stream; value and ms_per_step come from the median step. The flush keeps the device busy while the host
+enqueues the op pair, so the pair runs back to back as from a graph replay.
 
 value = algorithmic FLOPs per step / time per step, with F_alg = 6*B*H*D*T*(T+1) (12*D flop per causal
 (query, key) pair: 2 forward and 4 backward products; the backward's recompute of S is not counted).
 
 The JSON line also carries:
+  c_abi_warm_*  the same pair through the C ABI on preallocated outputs, back to back with warm caches
+                (op_warm_ms_per_step: through the ops, back to back; graph_ms_per_step: the C-ABI pair
+                replayed from a HIP graph; ref_method: graph replays after a flush, median / p20 / p80);
   roofline      the dominant kernel (the longest of the forward, dK/dV and dQ kernels), timed alone
                 with HIP events on the stream it is launched on: achieved = its algorithmic FLOPs per
                 launch (forward 4*D, dK/dV 6*D, dQ 2*D per causal pair) / its mean launch time, against
-                the dense BF16/FP16 MFMA peak of 2.5 PFLOP/s;
-  cpu_baseline  the reference's plain-PyTorch attention (repeat_interleave + SDPA math, forward +
-                autograd) in fp32 on the host cores, on a bounded sample of the same workload;
+                the dense BF16/FP16 MFMA peak of 2.5 PFLOP/s; traffic = its HBM bytes per launch from the
+                committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary of this workload;
+  cpu_baseline  the reference's plain-PyTorch attention on BASELINE config 1 (fp32, B=1, T=256), forward +
+                autograd backward, both of its forms (SDPA math and explicit matmuls), on the host CPUs;
   kernels       per-kernel mean times (nn_fa_bwd = the dQ kernel, which also runs the preprocessing pass,
                 then the dK/dV kernel) and the HBM rate of the standalone preprocessing entry point;
   layout_fusion the same fwd+bwd from (B, T, heads, hd) projections: through transposed views and the
@@ -107,7 +111,7 @@ def parse():
     p.add_argument("--kv-heads", type=int, default=4)
     p.add_argument("--head-dim", type=int, default=64)
     p.add_argument("--no-cpu-baseline", action="store_true")
-    p.add_argument("--cpu-seconds", type=float, default=10.0, help="budget of the CPU baseline sample")
+    p.add_argument("--cpu-seconds", type=float, default=16.0, help="budget of the CPU baseline sample (both forms)")
     p.add_argument("--profile-only", action="store_true", help="only the timed steps (for rocprofv3)")
     p.add_argument("--prewarm", type=float, default=1.0, help="seconds of untimed steps after the warmup")
     p.add_argument("--sweep", action="store_true",
@@ -126,6 +130,9 @@ SWEEP = [
     ("head_dim 32", 8, 1024, 12, 4, 32, "bf16", 1.0),
     ("MHA (12 KV heads)", 8, 1024, 12, 12, 64, "bf16", 1.0),
     ("MQA (1 KV head)", 8, 1024, 12, 1, 64, "bf16", 1.0),
+    # the reference benchmark's (B, T) ladder at fixed tokens (benchmarks/kernels/flash_attn.py:54); (8, 1024) is config 2
+    ("T=256 (ladder)", 32, 256, 12, 4, 64, "bf16", 1.0),
+    ("T=512 (ladder)", 16, 512, 12, 4, 64, "bf16", 1.0),
     ("T=2048", 4, 2048, 12, 4, 64, "bf16", 1.0),
     ("T=4096", 2, 4096, 12, 4, 64, "bf16", 1.0),
     ("T=16384", 1, 16384, 12, 4, 64, "bf16", 1.0),
@@ -189,11 +196,23 @@ def sweep(args):
         pairs = B * H * T * (T + 1) / 2
         reps = max(5, min(args.steps, int(30000 / events(step, 3))))  # about 30 ms of each measurement
         step_us = events(step, reps)
+        # the reference benchmark's method: each step after a 512 MiB cache flush, timed alone (median)
+        flush = torch.empty(512 << 20, dtype=torch.uint8, device=dev)
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(30)]
+        for i, (e0, e1) in enumerate(ev):
+            flush.fill_(i & 0xFF)
+            e0.record(stream)
+            step()
+            e1.record(stream)
+        torch.cuda.synchronize()
+        flushed_us = statistics.median(e0.elapsed_time(e1) for e0, e1 in ev) * 1e3
+        del flush
         us = {n: events(lambda fn=fn: check(fn()), reps) for n, fn in (("fwd", fwd), ("dq", dqk), ("dkdv", dkdv))}
         tf = lambda flop, t: round(flop / t / 1e6, 1)  # noqa: E731
         print(json.dumps({
             "shape": label, "B": B, "T": T, "H": H, "KVH": KVH, "D": D, "dtype": dts, "input_scale": mult,
             "step_us": round(step_us, 2), "tflops": tf(12 * D * pairs, step_us),
+            "flushed_step_us": round(flushed_us, 2), "flushed_tflops": tf(12 * D * pairs, flushed_us),
             "pct_of_peak": round(100 * 12 * D * pairs / step_us / 1e6 / PEAK_TFLOPS, 2),
             "fwd_us": round(us["fwd"], 2), "fwd_tflops": tf(4 * D * pairs, us["fwd"]),
             "dq_us": round(us["dq"], 2), "dq_tflops": tf(2 * D * pairs, us["dq"]),
@@ -203,52 +222,81 @@ def sweep(args):
         torch.cuda.empty_cache()
 
 
-def cpu_baseline(B, H, KVH, T, D, budget_s):
-    """Times the reference's plain-PyTorch CPU path (oracle.attention.torch_reference_fwd_bwd) in fp32.
+def _cpu_topology():
+    """(usable logical CPUs, physical cores among them, CPU model) of this host, from the process's CPU
+    affinity and /proc/cpuinfo (a core is a distinct (physical id, core id) pair)."""
+    usable = sorted(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else list(range(os.cpu_count() or 1))
+    model, cores, cur = platform.processor() or platform.machine(), set(), {}
+    try:
+        for line in open("/proc/cpuinfo"):
+            if ":" not in line:
+                if cur.get("processor") in usable:
+                    cores.add((cur.get("physical id", "0"), cur.get("core id", cur.get("processor"))))
+                cur = {}
+                continue
+            key, val = (x.strip() for x in line.split(":", 1))
+            if key == "processor":
+                cur["processor"] = int(val)
+            elif key in ("physical id", "core id"):
+                cur[key] = val
+            elif key == "model name":
+                model = val
+        if cur.get("processor") in usable:
+            cores.add((cur.get("physical id", "0"), cur.get("core id", cur.get("processor"))))
+    except OSError:
+        pass
+    return len(usable), len(cores) or len(usable), model
 
-    Sample: one batch element of the workload (B=1, same T, heads and head_dim), repeated for about
-    ``budget_s`` seconds after 3 warm-ups; the median time is scaled to TFLOP/s with the same
-    algorithmic FLOP count as the GPU figure.
+
+def cpu_baseline(budget_s):
+    """Times the reference's plain-PyTorch CPU path on BASELINE config 1, in the same process.
+
+    Config 1: fp32, B=1, T=256, 12 query / 4 KV heads, head_dim 64, torch.manual_seed(0) then randn q, k, v,
+    dO in that order, scale 1/sqrt(64). Both of the reference's forms (oracle.attention.torch_reference_fwd_bwd):
+    repeat_interleave + SDPA math (nanonemo/model/layers.py:109-115) and the explicit matmul / triu mask /
+    softmax form (tests/model/test_layers.py:107-123), each forward + autograd backward, timed for about
+    budget_s / 2 seconds after 3 warm-ups on every usable host CPU. The median of each is scaled to TFLOP/s
+    with the GPU figure's algorithmic FLOP count; ``value`` is the faster form.
     """
     import torch
 
     from oracle.attention import flops, torch_reference_fwd_bwd
 
-    threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or os.cpu_count() or 1
-    torch.set_num_threads(threads)
-    g = torch.Generator().manual_seed(0)
-    q = torch.randn(1, H, T, D, generator=g)
-    k = torch.randn(1, KVH, T, D, generator=g)
-    v = torch.randn(1, KVH, T, D, generator=g)
-    do = torch.randn(1, H, T, D, generator=g)
-    for _ in range(3):
-        torch_reference_fwd_bwd(q, k, v, do)
-    times = []
-    t_end = time.perf_counter() + budget_s
-    while time.perf_counter() < t_end or len(times) < 5:
-        t0 = time.perf_counter()
-        torch_reference_fwd_bwd(q, k, v, do)
-        times.append(time.perf_counter() - t0)
-        if len(times) >= 1000:
-            break
-    t = statistics.median(times)
-    cpu = platform.processor() or platform.machine()
-    try:
-        for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                cpu = line.split(":", 1)[1].strip()
+    B, H, KVH, T, D = 1, 12, 4, 256, 64
+    usable, phys, model = _cpu_topology()
+    torch.set_num_threads(usable)
+    torch.manual_seed(0)
+    q = torch.randn(B, H, T, D)
+    k = torch.randn(B, KVH, T, D)
+    v = torch.randn(B, KVH, T, D)
+    do = torch.randn(B, H, T, D)
+    forms = {}
+    for name, explicit in (("sdpa_math", False), ("explicit", True)):
+        for _ in range(3):
+            torch_reference_fwd_bwd(q, k, v, do, explicit=explicit)
+        times = []
+        t_end = time.perf_counter() + budget_s / 2
+        while time.perf_counter() < t_end or len(times) < 5:
+            t0 = time.perf_counter()
+            torch_reference_fwd_bwd(q, k, v, do, explicit=explicit)
+            times.append(time.perf_counter() - t0)
+            if len(times) >= 20000:
                 break
-    except OSError:
-        pass
+        t = statistics.median(times)
+        forms[name] = {"median_ms": round(t * 1e3, 4), "reps": len(times), "tflops": flops(B, H, T, D) / t / 1e12}
+    best = max(forms, key=lambda n: forms[n]["tflops"])
     return {
-        "value": flops(1, H, T, D) / t / 1e12,
+        "value": round(forms[best]["tflops"], 5),
         "unit": "TFLOP/s",
         "cores": torch.get_num_threads(),
         "kind": "port",
-        "sample": f"plain-PyTorch causal GQA (repeat_interleave + SDPA math) fwd+autograd bwd, fp32, "
-        f"B=1 of the workload (T={T}, {H}Q/{KVH}KV, d={D}); median of {len(times)} reps "
-        f"({sum(times):.1f} s) = {t * 1e3:.1f} ms",
-        "cpu_model": cpu,
+        "sample": f"BASELINE config 1: plain-PyTorch causal GQA fwd + autograd bwd, fp32, B={B} T={T} {H}Q/{KVH}KV "
+        f"d={D}, seed 0; value = the faster of the reference's two forms ({best}); medians over about "
+        f"{budget_s / 2:.0f} s each",
+        "forms": {n: {"median_ms": f["median_ms"], "reps": f["reps"], "tflops": round(f["tflops"], 5)} for n, f in forms.items()},
+        "threads": torch.get_num_threads(),
+        "physical_cores": phys,
+        "cpu_model": model,
     }
 
 
@@ -318,20 +366,44 @@ def main():
         torch.cuda.synchronize()
         return (time.perf_counter() - t0) * 1e3 / n
 
-    # Untimed: the W warmup steps of both paths (which make every allocation the timed steps reuse), then
+    # The last-level-cache flush of the reference benchmark's method (benchmarks/kernels/common.py:30-54): a
+    # 512 MiB write, twice the 256 MB Infinity Cache, before every timed step, so each step reads its inputs
+    # from HBM. Allocated before the warmup so that its allocation settles with the others.
+    flush = torch.empty(512 << 20, dtype=torch.uint8, device=dev)
+
+    def flushed_op_steps(n):
+        """n steps, each a cache flush and then the op pair timed alone with events on the launch stream.
+        The flush keeps the device busy for about 0.1 ms while the host enqueues the op pair behind it, so
+        the op pair runs back to back on the device as it would from a graph replay."""
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n)]
+        torch.cuda.synchronize()
+        for i, (a, b_) in enumerate(ev):
+            flush.fill_(i & 0xFF)
+            a.record(stream)
+            step_op()
+            b_.record(stream)
+        torch.cuda.synchronize()
+        return [a.elapsed_time(b_) for a, b_ in ev]
+
+    # Untimed: the W warmup steps of every path (which make every allocation the timed steps reuse), then
     # about 1 s of back-to-back steps. After a new device allocation the step time stays up to 15 %
     # longer for some 300 steps (~117 -> ~103 us at the default workload), so this settling run comes
     # after the last allocation and before the timed region.
     for _ in range(args.warmup):
         step_abi()
         step_op()
+    flushed_op_steps(max(args.warmup, 3))
     t_end = time.perf_counter() + args.prewarm
     while time.perf_counter() < t_end:
         for _ in range(200):  # the device never idles between these (the host runs ahead)
             step_abi()
         torch.cuda.synchronize()
-    # The headline: K steps through the C ABI, bracketed by device synchronisations.
-    ms = timed(step_abi, args.steps)
+    # The headline: K steps through the torch.library ops, each after a cache flush, bracketed by device
+    # synchronisations; value from the median step.
+    step_ms = flushed_op_steps(args.steps)
+    ms = statistics.median(step_ms)
+    # Beside it, warm-cache back-to-back steps: through the C ABI on resident outputs, and through the ops.
+    abi_ms = timed(step_abi, args.steps)
     op_ms = timed(step_op, args.steps)
     if args.profile_only:
         # The standalone preprocessing pass (nn_fa_bwd runs it fused into the dQ kernel), so that its
@@ -361,7 +433,8 @@ def main():
         for _ in range(3):
             dst.copy_(src)
         torch.cuda.synchronize()
-        print(json.dumps({"ms_per_step": ms, "op_ms_per_step": op_ms, "copy_calib_bytes": COPY_CALIB_BYTES}), flush=True)
+        print(json.dumps({"ms_per_step": ms, "c_abi_warm_ms_per_step": abi_ms, "op_warm_ms_per_step": op_ms,
+                          "copy_calib_bytes": COPY_CALIB_BYTES}), flush=True)
         return
 
 
@@ -482,7 +555,6 @@ def main():
     # The reference benchmark's method (benchmarks/kernels/common.py:30-54): every replay preceded by a
     # cache flush (a 512 MiB write, past the 256 MB Infinity Cache) and timed alone with events; median,
     # p20 and p80 over the replays.
-    flush = torch.empty(512 << 20, dtype=torch.uint8, device=dev)
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(max(100, args.steps))]
     for i, (a, b_) in enumerate(ev):
         flush.fill_(i & 0xFF)
@@ -491,7 +563,6 @@ def main():
         b_.record(stream)
     torch.cuda.synchronize()
     ref_ms = sorted(a.elapsed_time(b_) for a, b_ in ev)
-    del flush
 
     e = 2  # bytes per 16-bit element
     pre_alg_bytes = 2 * B * H * T * D * e + 4 * B * H * T
@@ -533,12 +604,22 @@ def main():
         "dtype": args.dtype,
         "data": "synthetic",
         "config": {
-            "workload": f"causal GQA attention fwd+bwd, B={B} T={T} {H}Q/{KVH}KV heads d={D} {args.dtype}, "
-            "one nn_fa_fwd + nn_fa_bwd C-ABI call pair per step on resident inputs",
+            "workload": f"causal GQA attention fwd+bwd, B={B} T={T} {H}Q/{KVH}KV heads d={D} {args.dtype}: one "
+            "nanonemo::flash_attn + nanonemo::flash_attn_bwd op pair per step on inputs resident in HBM, each step "
+            "after a 512 MiB last-level-cache flush and timed alone with HIP events (median of the K steps)",
             "B": B, "T": T, "H": H, "KVH": KVH, "D": D,
         },
         "pct_of_bf16_peak": round(100 * value / PEAK_TFLOPS, 2),
-        "op_ms_per_step": round(op_ms, 5),
+        "step_ms": {
+            "median": round(ms, 5),
+            "p20": round(sorted(step_ms)[len(step_ms) // 5], 5),
+            "p80": round(sorted(step_ms)[(4 * len(step_ms)) // 5], 5),
+            "mean": round(statistics.fmean(step_ms), 5),
+        },
+        # warm caches, back to back (the inputs stay in the 256 MB Infinity Cache between steps)
+        "c_abi_warm_ms_per_step": round(abi_ms, 5),
+        "c_abi_warm_tflops": round(f_all / (abi_ms * 1e-3) / 1e12, 2),
+        "op_warm_ms_per_step": round(op_ms, 5),
         "graph_ms_per_step": round(graph_ms, 5),
         "ref_method": {
             "how": "HIP-graph replay of the C-ABI step, each after a 512 MiB cache-flush write, timed alone with events",
@@ -594,7 +675,7 @@ def main():
         "device": {"name": props.name, "cus": props.multi_processor_count, "arch": getattr(props, "gcnArchName", "")},
     }
     if not args.no_cpu_baseline:
-        out["cpu_baseline"] = cpu_baseline(B, H, KVH, T, D, args.cpu_seconds)
+        out["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
     print(json.dumps(out), flush=True)
 
 

@@ -44,7 +44,11 @@ class ModelConfig:
     norm_eps: float = 1e-5
     rope_base: float = 10000.0
     init_std: float = 0.02
-    attn_backend: str = "math"  # SDPA backend of the "torch" attention
+    # SDPA backend of the "torch" attention: "math" and "mem_efficient" as in the reference (config.py:30),
+    # "math_fp32": the math backend on q, k, v upcast to fp32 (autocast off inside), output cast back; the
+    # reference attention that the tests and the config-5 comparison use (an fp32 reference, and no 16-bit
+    # batched products on transposed operands, which the math backend's forward and backward make)
+    attn_backend: str = "math"
     attn_kernel: str = "torch"  # "torch" | "hip" | "hip_bthd"
     rope_kernel: str = "torch"  # "torch" | "hip" (q and k rotated in one launch, nanonemo::rope_qk)
     norm_kernel: str = "torch"  # "torch" | "hip" (fused residual add + RMSNorm, nanonemo::cuda_add_rms_norm_*)
@@ -56,7 +60,7 @@ class ModelConfig:
             raise ValueError("query heads must group evenly over KV heads")
         if self.head_dim % 2:
             raise ValueError("RoPE rotates pairs of dimensions")
-        if self.attn_backend not in ("math", "mem_efficient"):
+        if self.attn_backend not in ("math", "mem_efficient", "math_fp32"):
             raise ValueError(f"unknown attn_backend {self.attn_backend!r}")
         if self.attn_kernel not in ("torch", "hip", "hip_bthd"):
             raise ValueError(f"unknown attn_kernel {self.attn_kernel!r}")
@@ -163,11 +167,14 @@ class Attention(nn.Module):
             y = self._fa.flash_attn(q, k, v)
         else:
             g = self.H // self.KVH
-            backend = {"math": SDPBackend.MATH, "mem_efficient": SDPBackend.EFFICIENT_ATTENTION}[self.cfg.attn_backend]
-            with sdpa_kernel(backend):
-                y = F.scaled_dot_product_attention(
-                    q, k.repeat_interleave(g, dim=1), v.repeat_interleave(g, dim=1), is_causal=True
-                )
+            kr, vr = k.repeat_interleave(g, dim=1), v.repeat_interleave(g, dim=1)
+            if self.cfg.attn_backend == "math_fp32":
+                with torch.autocast(q.device.type, enabled=False), sdpa_kernel(SDPBackend.MATH):
+                    y = F.scaled_dot_product_attention(q.float(), kr.float(), vr.float(), is_causal=True).to(q.dtype)
+            else:
+                backend = {"math": SDPBackend.MATH, "mem_efficient": SDPBackend.EFFICIENT_ATTENTION}[self.cfg.attn_backend]
+                with sdpa_kernel(backend):
+                    y = F.scaled_dot_product_attention(q, kr, vr, is_causal=True)
         return self.wo(y.transpose(1, 2).reshape(B, T, -1))
 
 

@@ -9,7 +9,14 @@ scaler are not needed here (bf16, one GPU).
 
 runs BASELINE config 5: the 114 M model, random init (seed 0), uniform synthetic token ids in
 [0, vocab), the same initial weights and batches for every attention kernel, and prints one JSON line
-with tokens/s per kernel and the largest per-step loss difference from the "torch" (SDPA) path.
+with tokens/s per kernel and each kernel's loss curve against the "torch" (SDPA) path's.
+
+The curve check, with its bounds in the JSON: step 0 (identical weights and batch, before any update)
+within STEP0_BOUND of the torch loss, which is the per-step parity the GPU tests pin; and every one of the
+50 steps within CURVE_BOUND (about 1 % of the loss, ln 50304 = 10.83 on uniform tokens). Two bf16 runs
+with different kernels drift apart as the updates diverge, so the later steps are bounded by the drift
+two parity-green attention builds show against each other (up to about 0.09 here), not by the per-step
+tolerance.
 """
 
 from __future__ import annotations
@@ -21,6 +28,9 @@ import time
 import torch
 
 from nanonemo_amd.model import ModelConfig, NanoNemo
+
+STEP0_BOUND = 5e-3
+CURVE_BOUND = 0.12
 
 
 def train_step(model, opt, batches, grad_clip: float = 1.0, amp_dtype=torch.bfloat16):
@@ -95,9 +105,12 @@ def main():
     p.add_argument("--attn", nargs="+", default=["torch", "hip", "hip_bthd", "hip_bthd+rope", "hip_bthd+rope+norm"],
                    help="attention kernels; '+rope' / '+norm' suffixes also select the HIP RoPE / add+RMSNorm kernels")
     p.add_argument("--small", action="store_true", help="a 2-layer model (quick check)")
+    p.add_argument("--torch-backend", default="math_fp32", choices=["math", "mem_efficient", "math_fp32"],
+                   help="SDPA backend of the torch attention (math_fp32: fp32 math on upcast q, k, v)")
     a = p.parse_args()
     cfg_kwargs = dict(n_layers=2, d_model=256, n_heads=4, n_kv_heads=2, d_ff=512, vocab_size=512, max_seq_len=a.seq) \
         if a.small else dict(max_seq_len=a.seq)
+    cfg_kwargs["attn_backend"] = a.torch_backend
     res = {}
     for attn in a.attn:
         losses, tps, fpt = run(attn, a.steps, a.batch, a.seq, cfg_kwargs)
@@ -108,9 +121,14 @@ def main():
         for attn in res:
             if attn != "torch":
                 d = [abs(x - y) for x, y in zip(res[attn]["losses"], res["torch"]["losses"])]
+                res[attn]["step0_abs_loss_diff_vs_torch"] = round(d[0], 6)
                 res[attn]["max_abs_loss_diff_vs_torch"] = round(max(d), 5)
+                res[attn]["first_step_past_0.01"] = next((i for i, x in enumerate(d) if x > 0.01), None)
+                res[attn]["curve_within_bounds"] = bool(d[0] <= STEP0_BOUND and max(d) <= CURVE_BOUND)
     print(json.dumps({"workload": f"114M NanoNemo bf16 autocast, B={a.batch} T={a.seq}, {a.steps} AdamW steps, "
-                      "seed 0, uniform synthetic tokens", "results": res}), flush=True)
+                      f"seed 0, uniform synthetic tokens; torch attention: SDPA {a.torch_backend}",
+                      "bounds": {"step0_abs_loss_diff": STEP0_BOUND, "max_abs_loss_diff": CURVE_BOUND},
+                      "results": res}), flush=True)
 
 
 if __name__ == "__main__":

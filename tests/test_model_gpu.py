@@ -13,17 +13,21 @@ from nanonemo_amd.train import make_optimizer, synthetic_batches, train_step
 
 pytestmark = pytest.mark.gpu
 
-SMALL = dict(n_layers=2, d_model=256, n_heads=4, n_kv_heads=2, d_ff=512, vocab_size=512, max_seq_len=128)
+# attn_backend only affects the "torch" attention: the reference model attends in fp32 (SDPA math on upcast q, k, v)
+SMALL = dict(n_layers=2, d_model=256, n_heads=4, n_kv_heads=2, d_ff=512, vocab_size=512, max_seq_len=128,
+             attn_backend="math_fp32")
 
 
-def _pair(attn: str):
-    """The plain model and one with this build's kernels ("+norm": also the fused add + RMSNorm)."""
+def _pair(attn: str, cfg: dict = SMALL, batch: int = 2):
+    """The plain model and one with this build's kernels ("+rope" / "+norm": also the HIP RoPE / fused add +
+    RMSNorm), on identical weights, with a batch of uniform token ids and their next-token targets."""
     kernel, *extras = attn.split("+")
     torch.manual_seed(0)
-    ref = NanoNemo(ModelConfig(**SMALL)).cuda()
-    fast = NanoNemo(ModelConfig(**SMALL, attn_kernel=kernel, norm_kernel="hip" if "norm" in extras else "torch")).cuda()
+    ref = NanoNemo(ModelConfig(**cfg)).cuda()
+    fast = NanoNemo(ModelConfig(**cfg, attn_kernel=kernel, rope_kernel="hip" if "rope" in extras else "torch",
+                                norm_kernel="hip" if "norm" in extras else "torch")).cuda()
     fast.load_state_dict(ref.state_dict())
-    idx = torch.randint(0, SMALL["vocab_size"], (2, 128), device="cuda")
+    idx = torch.randint(0, ref.cfg.vocab_size, (batch, ref.cfg.max_seq_len), device="cuda")
     return ref, fast, idx, torch.roll(idx, -1, dims=1)
 
 
@@ -45,6 +49,36 @@ def test_bf16_autocast_loss_and_grads_match_torch_attention(attn):
     for name, g in _grads(fast).items():
         r = _grads(ref)[name]
         torch.testing.assert_close(g, r, rtol=5e-2, atol=5e-2 * r.abs().max().item(), msg=name)
+
+
+# the full 114 M model (12 layers, d_model 768, 12 Q / 4 KV heads, SwiGLU 2048, vocab 50,304,
+# tied embeddings) at B=8, T=1024 under bf16 autocast, random init (seed 0), uniform token ids.
+CONFIG5 = dict(max_seq_len=1024, attn_backend="math_fp32")
+
+
+@pytest.mark.parametrize("attn", ["hip_bthd", "hip", "hip_bthd+rope+norm"])
+def test_config5_full_size_loss_and_grads_match_torch_attention(attn):
+    # The pattern of /root/reference/tests/kernels/test_model_kernels.py:54-66 (loss 1e-3, every gradient within
+    # 5e-2 of its largest magnitude) at the full model and batch, widened for bf16: loss 5e-3.
+    print(f"\n[case] config 5 full size, {attn} vs torch attention (fp32 math), bf16 autocast", flush=True)
+    ref, fast, idx, tgt = _pair(attn, CONFIG5, batch=8)
+    assert ref.num_params() == 114_150_144
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        _, ref_loss = ref(idx, tgt)
+        _, loss = fast(idx, tgt)
+    print(f"[loss] torch {ref_loss.item():.6f} {attn} {loss.item():.6f}", flush=True)
+    torch.testing.assert_close(loss, ref_loss, rtol=5e-3, atol=5e-3)
+    ref_loss.backward()
+    loss.backward()
+    worst = 0.0
+    for name, g in _grads(fast).items():
+        r = _grads(ref)[name]
+        assert g is not None and torch.isfinite(g).all(), name
+        worst = max(worst, ((g - r).abs().max() / r.abs().max()).item())
+        torch.testing.assert_close(g, r, rtol=5e-2, atol=5e-2 * r.abs().max().item(), msg=name)
+    print(f"[grads] largest |g - ref| / max|ref| over parameters: {worst:.3e}", flush=True)
+    del ref, fast
+    torch.cuda.empty_cache()
 
 
 def test_layout_fused_model_is_bit_identical_to_the_drop_in_model():

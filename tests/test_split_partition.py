@@ -1,0 +1,109 @@
+"""Index-level emulation (CPU) of the backward's workspace and of the split dK/dV partition.
+
+Restates, for the host and the kernels in nanonemo_amd/csrc/flash_attn.hip, only the index arithmetic:
+carve() (where -D, -lse/scale and the split partials sit in the workspace), dkdv_split(), the dK/dV kernel's
+block -> (split, unit pair) mapping, each split's iteration range [s n / S, (s + 1) n / S) of a unit, the
+chunk-owner reduction's part[] stores, and the sum kernel's part[] reads. It proves, per shape:
+  * every part element the sum kernel reads is stored by exactly one block of the same split in the dK/dV
+    launch (so no element is read before it is written in stream order, and none is written twice);
+  * every (query head, query tile) iteration of every unit is taken by exactly one (split, wave);
+  * the three workspace regions are disjoint, 256-byte aligned, inside the size the library reports.
+The kernels exchange data only through these buffers and only across kernel boundaries (dQ writes -D and
+-lse/scale, dK/dV reads them and writes part, the sum kernel reads part); no block reads what another block
+of the same launch writes. The shape (B=2, H=12, KVH=1, T=1024, D=64, 16 splits) is the one whose first HIP
+graph replay once differed from the eager result.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from nanonemo_amd.kernels.hip import lib
+
+
+def round256(n):
+    return (n + 255) & ~255
+
+
+def dkdv_split(B, H, KVH, T):
+    nkb = (T + 63) // 64
+    base = B * KVH * ((nkb + 1) // 2)
+    if base >= 256 or (H // KVH) * nkb * 16 >= 2**31:
+        return 1
+    return max(1, min(16, -(-256 // base), (H // KVH) * (nkb + 1) // 8))
+
+
+def carve(B, H, KVH, T, D):
+    vec = round256(4 * B * H * T)
+    S = dkdv_split(B, H, KVH, T)
+    regions = {"nD": (0, 4 * B * H * T), "nL": (vec, vec + 4 * B * H * T)}
+    if S > 1:
+        regions["part"] = (2 * vec, 2 * vec + S * 2 * 4 * B * KVH * T * D)
+    total = 2 * vec + (round256(S * 2 * 4 * B * KVH * T * D) if S > 1 else 0)
+    return S, regions, total
+
+
+def emulate_split(B, H, KVH, T, D):
+    """Returns (store count per part element, iteration owner count per (bk, unit, iteration))."""
+    S = dkdv_split(B, H, KVH, T)
+    nkb = nqt = (T + 63) // 64
+    npairs = (nkb + 1) // 2
+    BKV, group, WPP, NW = B * KVH, H // KVH, 4, 4  # a split launch always runs 4 waves per pair
+    ND = D // 32
+    nbk = BKV  # PPB = 1
+    nbase = nbk * npairs
+    stores = np.zeros((S, 2, BKV, T, D), dtype=np.int32)
+    owners = {}
+    for block in range(nbk * npairs * S):
+        sidx, bid = divmod(block, nbase)
+        bgrp, pj = bid % nbk, bid // nbk
+        bk = bgrp
+        units = [pj] if nkb - 1 - pj == pj else [pj, nkb - 1 - pj]
+        for unit in units:
+            n = group * (nqt - unit)
+            first, end = sidx * n // S, (sidx + 1) * n // S
+            for wp in range(WPP):
+                for itn in range(first + wp, end, WPP):
+                    owners[(bk, unit, itn)] = owners.get((bk, unit, itn), 0) + 1
+            kb0 = unit * 64
+            for which in range(2):  # dK, then dV: every chunk c (its owner wave c % 4) stores 4 columns per lane
+                for c in range(2 * ND * 4):
+                    for lane in range(64):
+                        l32, hh = lane & 31, lane >> 5
+                        key = kb0 + 32 * (c // (4 * ND)) + l32
+                        col = 32 * (c // 4 % ND) + 8 * (c % 4) + 4 * hh
+                        if key < T:
+                            stores[sidx, which, bk, key, col:col + 4] += 1
+    return S, stores, owners, nkb, nqt, group, BKV
+
+
+SHAPES = [(2, 12, 1, 1024, 64), (8, 12, 1, 1024, 64), (1, 12, 4, 1024, 64), (1, 12, 4, 400, 32), (2, 6, 2, 333, 64)]
+
+
+@pytest.mark.parametrize("shape", SHAPES)
+def test_split_partials_are_each_stored_once_and_every_iteration_is_taken_once(shape):
+    B, H, KVH, T, D = shape
+    S, stores, owners, nkb, nqt, group, BKV = emulate_split(B, H, KVH, T, D)
+    assert S > 1, "the shapes here all split"
+    # the sum kernel reads part[s][which][bk][key][col] for every s < S, key < T, col < D: each stored exactly once
+    assert stores.min() == 1 and stores.max() == 1
+    want = {(bk, u, i) for bk in range(BKV) for u in range(nkb) for i in range(group * (nqt - u))}
+    assert set(owners) == want and all(v == 1 for v in owners.values())
+
+
+@pytest.mark.parametrize("shape", SHAPES + [(8, 12, 4, 1024, 64), (32, 12, 4, 1024, 64), (1, 1, 1, 1, 32)])
+def test_workspace_regions_are_disjoint_aligned_and_sized_as_the_library_says(shape):
+    B, H, KVH, T, D = shape
+    S, regions, total = carve(B, H, KVH, T, D)
+    assert lib().nn_fa_bwd_workspace_size(B, H, KVH, T, D) == total
+    spans = sorted(regions.values())
+    for (a0, a1), (b0, b1) in zip(spans, spans[1:]):
+        assert a1 <= b0, regions
+    assert all(lo % 256 == 0 and hi <= total for lo, hi in spans)
+
+
+def test_the_replay_shape_splits_sixteen_ways():
+    S, regions, total = carve(2, 12, 1, 1024, 64)
+    assert S == 16 and set(regions) == {"nD", "nL", "part"}
+    assert regions["part"][1] - regions["part"][0] == 16 * 2 * 4 * 2 * 1 * 1024 * 64
