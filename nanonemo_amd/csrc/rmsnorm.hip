@@ -1,24 +1,34 @@
 // Fused residual add + RMSNorm, forward and backward, for MI355X (gfx950).
 //
-// Semantics of the reference's fused kernel (/root/reference/nanonemo/kernels/cuda/rmsnorm.cu, op
-// wrapper rmsnorm.py) and of the plain-PyTorch blocks it replaces (nanonemo/model/layers.py:19-56):
-//     h = x + delta (rounded to h's dtype, the promotion of x's and delta's),
-//     y = (h * rstd) * w,   rstd = 1 / sqrt(mean(h^2) + eps)            (fp32, rounded once to y's dtype)
-// and, with n = h * rstd and dn = dy * w,
-//     dh = rstd * (dn - n * mean(dn * n)) + dh_residual,   dw = sum over rows of dy * n.
-// delta may be absent (y = rmsnorm(x); h is then x itself and is not written).
+// What it computes (the plain-PyTorch blocks of /root/reference/nanonemo/model/layers.py:19-56 and the
+// reference's fused op, kernels/cuda/rmsnorm.py):
+//     h = x + delta, rounded to h's dtype (the promotion of x's and delta's); h is x when there is no delta
+//     r = 1 / sqrt(mean(h^2) + eps),   y = (h * r) * w          (fp32 arithmetic, y rounded once)
+// and its gradient, with g = dy * w:
+//     dh_total = r * g - h * (r^3 * sum(g * h) / N)  (+ dh, the gradient reaching h from the residual)
+//     dw = sum over rows of dy * h * r
+// (the derivative of y with respect to h: r g minus the projection of r g on h's direction).
 //
-// Layout: M rows of N contiguous elements. One wave64 per row (4 rows per 256-thread block); a lane
-// owns 8-element chunks lane, lane + 64, ... (16-byte loads for the 16-bit types, two for fp32) and
-// keeps its row in registers between the reduction and the write, so every input is read once and
-// every output written once (N a multiple of 8 up to 4096; any other N up to 1024 takes single
-// elements instead). The backward walks two rows per wave at a time where they fit (N <= 2048). The
-// sums of squares and of dn * n are butterfly reductions over the wave (deterministic). The
-// backward's dw is reduced per block (its 4 waves through LDS) into a [blocks][N] fp32 workspace,
-// then summed over blocks in a fixed order by a second kernel: no atomics, bit-reproducible.
+// Work decomposition. A row is owned by a *team* of R lanes: in the backward R = 32 for up to 128 16-byte
+// vectors per row (N <= 1024) and R = 64 above (N <= 4096); the forward uses R = 64 throughout. A wave holds
+// 64 / R rows. Lane t of a team owns the vectors t, t + R, ..., t + (K - 1) R of its row (K = ceil(vectors /
+// R), from a small set of counts; a vector past the row's end is never loaded or stored), so each load
+// instruction of a team reads R consecutive 16-byte vectors and the row sits in registers from its loads to
+// its stores. At the model's width (N = 768: 96 vectors) a backward team of 32 lanes holds exactly 3 vectors
+// per lane and a wave 2 rows.
+// Widths that are not a multiple of 8 (up to 1024) use a 64-lane team of single elements.
+// Team sums are xor-butterflies over the team's lanes (deterministic). Every load a row needs (and the
+// weight, first) is issued before its first use, so one memory latency covers the row.
 //
-// Element types are a launch-uniform runtime code (0 fp16, 1 bf16, 2 fp32) resolved inside the
-// load / store helpers: the kernel is HBM-bound, and the switch is a scalar branch per chunk.
+// Backward. A fixed grid of at most kBwdBlocks blocks of 8 waves; every team walks rows team_id,
+// team_id + teams, ... and keeps its lanes' dw contributions in registers across all of them. At the
+// end the teams of a wave are summed by an xor-butterfly over their lane groups, the block's waves in
+// LDS in wave order into one fp32 partial row per block, and colsum_kernel adds the partial rows in
+// block order (16 waves per 64 columns, each wave a fixed stride of rows, then the 16 wave sums in
+// order): dw without atomics, bit-reproducible, and no memset (M = 0 writes zeros).
+//
+// Element types are runtime codes (0 fp16, 1 bf16, 2 fp32), uniform per launch, converted to fp32 at
+// the load and rounded at the store: the kernels are HBM-bound, so a uniform branch per vector is free.
 #include <hip/hip_runtime.h>
 #include <stdarg.h>
 #include <stdint.h>
@@ -36,270 +46,278 @@ namespace {
 using u16 = unsigned short;
 typedef u16 u16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 
 constexpr int kF16 = 0, kBF16 = 1, kF32 = 2;
-constexpr int kRows = 4;          // rows (waves) per block
-constexpr int kBwdBlocks = 1024;  // most blocks of the backward; each owns a range of rows
+constexpr int kWaves = 4;         // waves per block of the forward
+constexpr int kBwdWaves = 8;      // waves per block of the backward
+constexpr int kBwdBlocks = 512;   // most blocks of the backward (each then owns one dw partial row)
+constexpr int kSumWaves = 16;     // waves of a column-sum block
 
 __host__ __device__ inline int elem_bytes(int dt) { return dt == kF32 ? 4 : 2; }
 
-// V consecutive elements at element index i of a row-major array of type dt, to / from fp32.
-template <int V>
-__device__ inline void load(const char* base, long long i, int dt, float* v) {
-    if constexpr (V == 8) {
-        if (dt == kF32) {
-            const f32x4* p = reinterpret_cast<const f32x4*>(base + i * 4);
-            const f32x4 a = p[0], b = p[1];
-#pragma unroll
-            for (int j = 0; j < 4; ++j) v[j] = a[j], v[j + 4] = b[j];
-        } else {
-            const u16x8 w = *reinterpret_cast<const u16x8*>(base + i * 2);
-            if (dt == kBF16) {
-#pragma unroll
-                for (int j = 0; j < 8; ++j) v[j] = __uint_as_float((uint32_t)w[j] << 16);
-            } else {
-                const f16x8 hv = __builtin_bit_cast(f16x8, w);
-#pragma unroll
-                for (int j = 0; j < 8; ++j) v[j] = (float)hv[j];
-            }
-        }
-    } else {
-        if (dt == kF32)
-            v[0] = reinterpret_cast<const float*>(base)[i];
-        else if (dt == kBF16)
-            v[0] = __uint_as_float((uint32_t)reinterpret_cast<const u16*>(base)[i] << 16);
-        else
-            v[0] = (float)reinterpret_cast<const _Float16*>(base)[i];
+// Vector j (8 elements) of a row-major array of element type dt, widened to fp32.
+__device__ inline f32x8 load_vec(const void* base, long long j, int dt) {
+    if (dt == kF32) {
+        const f32x4* p = reinterpret_cast<const f32x4*>(base) + 2 * j;
+        const f32x4 a = p[0], b = p[1];
+        return f32x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
     }
-}
-
-template <int V>
-__device__ inline void store(char* base, long long i, int dt, const float* v) {  // round to nearest even
-    if constexpr (V == 8) {
-        if (dt == kF32) {
-            f32x4* p = reinterpret_cast<f32x4*>(base + i * 4);
-            p[0] = f32x4{v[0], v[1], v[2], v[3]};
-            p[1] = f32x4{v[4], v[5], v[6], v[7]};
-        } else if (dt == kBF16) {
-            bf16x8 r;
+    const u16x8 raw = reinterpret_cast<const u16x8*>(base)[j];
+    f32x8 v;
+    if (dt == kBF16) {
 #pragma unroll
-            for (int j = 0; j < 8; ++j) r[j] = (__bf16)v[j];
-            *reinterpret_cast<u16x8*>(base + i * 2) = __builtin_bit_cast(u16x8, r);
-        } else {
-            f16x8 r;
-#pragma unroll
-            for (int j = 0; j < 8; ++j) r[j] = (_Float16)v[j];
-            *reinterpret_cast<u16x8*>(base + i * 2) = __builtin_bit_cast(u16x8, r);
-        }
+        for (int e = 0; e < 8; ++e) v[e] = __uint_as_float((uint32_t)raw[e] << 16);
     } else {
-        if (dt == kF32)
-            reinterpret_cast<float*>(base)[i] = v[0];
-        else if (dt == kBF16)
-            reinterpret_cast<__bf16*>(base)[i] = (__bf16)v[0];
-        else
-            reinterpret_cast<_Float16*>(base)[i] = (_Float16)v[0];
-    }
-}
-
-// fp32 value rounded to dtype dt and widened back (the value a store of dt would hold).
-__device__ inline float round_to(float x, int dt) {
-    if (dt == kBF16) return (float)(__bf16)x;
-    if (dt == kF16) return (float)(_Float16)x;
-    return x;
-}
-
-__device__ inline float wave_sum(float v) {
+        const f16x8 hv = __builtin_bit_cast(f16x8, raw);
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+        for (int e = 0; e < 8; ++e) v[e] = (float)hv[e];
+    }
     return v;
 }
 
-// y, h, rstd of rows blockIdx.x * 4 + wave. Chunk i of a lane: elements (lane + 64 i) * V ...
-template <int V, int MAXC, bool HAS_DELTA>
-__global__ __launch_bounds__(256) void add_rmsnorm_fwd_kernel(const char* __restrict__ x, const char* __restrict__ d,
-                                                              const float* __restrict__ w, char* __restrict__ y,
-                                                              char* __restrict__ h, float* __restrict__ rstd_out,
-                                                              long long M, int N, float eps, int xdt, int ddt, int hdt,
-                                                              int ydt) {
-    const long long row = (long long)blockIdx.x * kRows + (threadIdx.x >> 6);
-    const int lane = threadIdx.x & 63;
-    if (row >= M) return;  // the whole wave
-    const int chunks = N / V;
-    float v[MAXC][V];
+// Vector j of a row-major array of type dt from fp32, rounded to nearest even.
+__device__ inline void store_vec(void* base, long long j, int dt, const f32x8& v) {
+    if (dt == kF32) {
+        f32x4* p = reinterpret_cast<f32x4*>(base) + 2 * j;
+        p[0] = f32x4{v[0], v[1], v[2], v[3]};
+        p[1] = f32x4{v[4], v[5], v[6], v[7]};
+    } else if (dt == kBF16) {
+        bf16x8 r;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) r[e] = (__bf16)v[e];
+        reinterpret_cast<u16x8*>(base)[j] = __builtin_bit_cast(u16x8, r);
+    } else {
+        f16x8 r;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) r[e] = (_Float16)v[e];
+        reinterpret_cast<u16x8*>(base)[j] = __builtin_bit_cast(u16x8, r);
+    }
+}
+
+__device__ inline float load_one(const void* base, long long i, int dt) {
+    if (dt == kF32) return reinterpret_cast<const float*>(base)[i];
+    const u16 raw = reinterpret_cast<const u16*>(base)[i];
+    return dt == kBF16 ? __uint_as_float((uint32_t)raw << 16) : (float)__builtin_bit_cast(_Float16, raw);
+}
+
+__device__ inline void store_one(void* base, long long i, int dt, float v) {
+    if (dt == kF32)
+        reinterpret_cast<float*>(base)[i] = v;
+    else if (dt == kBF16)
+        reinterpret_cast<__bf16*>(base)[i] = (__bf16)v;
+    else
+        reinterpret_cast<_Float16*>(base)[i] = (_Float16)v;
+}
+
+// The value a store to dtype dt would keep.
+__device__ inline float keep_as(float v, int dt) {
+    return dt == kBF16 ? (float)(__bf16)v : dt == kF16 ? (float)(_Float16)v : v;
+}
+
+// Sum over the R lanes of a team (R a power of two, teams aligned to R lanes).
+template <int R>
+__device__ inline float team_sum(float v) {
+#pragma unroll
+    for (int m = R / 2; m > 0; m >>= 1) v += __shfl_xor(v, m);
+    return v;
+}
+
+// A row's slice held by one lane: K units of W elements (W = 8: 16-byte vectors; W = 1: single
+// elements); unit k is the row's unit t + k R.
+template <int W, int K>
+struct Slice {
+    float v[K][W];
+};
+
+template <int W, int K, int R>
+__device__ inline void load_slice(const void* row, int dt, int t, int units, Slice<W, K>& s) {
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+        const int u = t + k * R;
+        if constexpr (W == 8) {
+            const f32x8 x = u < units ? load_vec(row, u, dt) : f32x8{};
+#pragma unroll
+            for (int e = 0; e < 8; ++e) s.v[k][e] = x[e];
+        } else {
+            s.v[k][0] = u < units ? load_one(row, u, dt) : 0.f;
+        }
+    }
+}
+
+template <int W, int K, int R>
+__device__ inline void store_slice(void* row, int dt, int t, int units, const Slice<W, K>& s) {
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+        const int u = t + k * R;
+        if (u >= units) continue;
+        if constexpr (W == 8) {
+            f32x8 x;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) x[e] = s.v[k][e];
+            store_vec(row, u, dt, x);
+        } else {
+            store_one(row, u, dt, s.v[k][0]);
+        }
+    }
+}
+
+// The weight's units of this lane (fp32 [N]).
+template <int W, int K, int R>
+__device__ inline void load_weight(const float* w, int t, int units, Slice<W, K>& s) {
+    load_slice<W, K, R>(w, kF32, t, units, s);
+}
+
+// ------------------------------------------------------------------------------------------
+// Forward: one row per team, 4 waves per block.
+// ------------------------------------------------------------------------------------------
+template <int W, int K, int R, bool DELTA>
+__global__ __launch_bounds__(64 * kWaves) void add_rmsnorm_fwd_kernel(const void* __restrict__ x,
+                                                                       const void* __restrict__ delta,
+                                                                       const float* __restrict__ w,
+                                                                       void* __restrict__ y, void* __restrict__ h,
+                                                                       float* __restrict__ rstd, long long M, int N,
+                                                                       float eps, int xdt, int ddt, int hdt, int ydt) {
+    constexpr int TPB = 64 * kWaves / R;  // teams (rows) per block
+    const int team = threadIdx.x / R, t = threadIdx.x % R;
+    const long long row = (long long)blockIdx.x * TPB + team;
+    if (row >= M) return;  // a whole team leaves together (teams never straddle a row)
+    const int units = N / W;
+    const long long off = row * N;  // element offset of the row
+    const int xb = elem_bytes(xdt);
+
+    Slice<W, K> hv, wv, dv;
+    load_weight<W, K, R>(w, t, units, wv);
+    load_slice<W, K, R>((const char*)x + off * xb, xdt, t, units, hv);
+    if constexpr (DELTA) load_slice<W, K, R>((const char*)delta + off * elem_bytes(ddt), ddt, t, units, dv);
+    if constexpr (DELTA) {
+#pragma unroll
+        for (int k = 0; k < K; ++k)
+#pragma unroll
+            for (int e = 0; e < W; ++e) hv.v[k][e] = keep_as(hv.v[k][e] + dv.v[k][e], hdt);
+        store_slice<W, K, R>((char*)h + off * elem_bytes(hdt), hdt, t, units, hv);
+    }
     float ss = 0.f;
 #pragma unroll
-    for (int i = 0; i < MAXC; ++i) {
-        const int c = lane + 64 * i;
-        if (c >= chunks) break;
-        const long long off = row * N + (long long)c * V;
-        load<V>(x, off, xdt, v[i]);
-        if constexpr (HAS_DELTA) {
-            float dv[V];
-            load<V>(d, off, ddt, dv);
+    for (int k = 0; k < K; ++k)
 #pragma unroll
-            for (int j = 0; j < V; ++j) v[i][j] = round_to(v[i][j] + dv[j], hdt);  // the residual as stored
-            store<V>(h, off, hdt, v[i]);
-        }
+        for (int e = 0; e < W; ++e) ss = fmaf(hv.v[k][e], hv.v[k][e], ss);
+    const float r = rsqrtf(team_sum<R>(ss) / (float)N + eps);
 #pragma unroll
-        for (int j = 0; j < V; ++j) ss += v[i][j] * v[i][j];
+    for (int k = 0; k < K; ++k)
+#pragma unroll
+        for (int e = 0; e < W; ++e) hv.v[k][e] = (hv.v[k][e] * r) * wv.v[k][e];
+    store_slice<W, K, R>((char*)y + off * elem_bytes(ydt), ydt, t, units, hv);
+    if (t == 0) rstd[row] = r;
+}
+
+// ------------------------------------------------------------------------------------------
+// Backward: a fixed grid; each team walks rows team_id + i * teams, keeping dw in registers; then the
+// teams of a wave are summed over their lane groups and the block's waves in LDS into partial row
+// blockIdx.x.
+// ------------------------------------------------------------------------------------------
+template <int W, int K, int R, bool DELTA>
+__global__ __launch_bounds__(64 * kBwdWaves) void add_rmsnorm_bwd_kernel(
+    const void* __restrict__ dy, const void* __restrict__ dh, const void* __restrict__ h, const float* __restrict__ w,
+    const float* __restrict__ rstd, void* __restrict__ dx, void* __restrict__ ddelta, float* __restrict__ dw_part,
+    long long M, int N, int dydt, int hdt, int dxdt, int dddt) {
+    constexpr int TPB = 64 * kBwdWaves / R;
+    __shared__ float red[kBwdWaves][K * R * W];  // each wave's dw, unit-major per lane position
+    const int team = threadIdx.x / R, t = threadIdx.x % R, wave = threadIdx.x >> 6;
+    const int units = N / W;
+    const long long teams = (long long)gridDim.x * TPB;
+    const int dyb = elem_bytes(dydt), hb = elem_bytes(hdt);
+
+    Slice<W, K> wv, acc;
+    load_weight<W, K, R>(w, t, units, wv);
+#pragma unroll
+    for (int k = 0; k < K; ++k)
+#pragma unroll
+        for (int e = 0; e < W; ++e) acc.v[k][e] = 0.f;
+
+    for (long long row = (long long)blockIdx.x * TPB + team; row < M; row += teams) {
+        const long long off = row * N;
+        Slice<W, K> gv, hv, res;  // dy (then g, then the gradient), h, and dh
+        load_slice<W, K, R>((const char*)dy + off * dyb, dydt, t, units, gv);
+        load_slice<W, K, R>((const char*)h + off * hb, hdt, t, units, hv);
+        if constexpr (DELTA) load_slice<W, K, R>((const char*)dh + off * hb, hdt, t, units, res);
+        const float r = rstd[row];
+        float s = 0.f;
+#pragma unroll
+        for (int k = 0; k < K; ++k)
+#pragma unroll
+            for (int e = 0; e < W; ++e) {
+                acc.v[k][e] = fmaf(gv.v[k][e], hv.v[k][e] * r, acc.v[k][e]);  // dw += dy * (h r)
+                gv.v[k][e] *= wv.v[k][e];                                     // g = dy * w
+                s = fmaf(gv.v[k][e], hv.v[k][e], s);
+            }
+        const float c = r * r * r * team_sum<R>(s) / (float)N;
+#pragma unroll
+        for (int k = 0; k < K; ++k)
+#pragma unroll
+            for (int e = 0; e < W; ++e) {
+                const float d = gv.v[k][e] * r - hv.v[k][e] * c;
+                gv.v[k][e] = DELTA ? d + res.v[k][e] : d;
+            }
+        store_slice<W, K, R>((char*)dx + off * elem_bytes(dxdt), dxdt, t, units, gv);
+        if constexpr (DELTA) store_slice<W, K, R>((char*)ddelta + off * elem_bytes(dddt), dddt, t, units, gv);
     }
-    const float rstd = 1.f / sqrtf(wave_sum(ss) / (float)N + eps);
-    if (lane == 0) rstd_out[row] = rstd;
+
+    // The wave's teams hold the same columns in lanes t, t + R, ...: an xor-butterfly over those lane
+    // groups leaves every lane with the wave's sum.
 #pragma unroll
-    for (int i = 0; i < MAXC; ++i) {
-        const int c = lane + 64 * i;
-        if (c >= chunks) break;
-        float o[V];
-        load<V>(reinterpret_cast<const char*>(w), (long long)c * V, kF32, o);
+    for (int k = 0; k < K; ++k)
 #pragma unroll
-        for (int j = 0; j < V; ++j) o[j] *= v[i][j] * rstd;
-        store<V>(y, row * N + (long long)c * V, ydt, o);
+        for (int e = 0; e < W; ++e) {
+            float a = acc.v[k][e];
+#pragma unroll
+            for (int m = R; m < 64; m <<= 1) a += __shfl_xor(a, m);
+            if ((threadIdx.x & 63) < R) red[wave][(k * R + t) * W + e] = a;
+        }
+    __syncthreads();
+    // Unit-major columns: element (k R + t) W + e of a wave's slot is column (t + k R) W + e.
+    for (int i = threadIdx.x; i < K * R * W; i += 64 * kBwdWaves) {
+        const int kk = i / (R * W), rem = i - kk * R * W, tt = rem / W, e = rem - tt * W;
+        const int col = (tt + kk * R) * W + e;
+        if (col >= N) continue;
+        float sum = 0.f;
+#pragma unroll
+        for (int m = 0; m < kBwdWaves; ++m) sum += red[m][i];
+        dw_part[(long long)blockIdx.x * N + col] = sum;
     }
 }
 
-// Rows [blockIdx.x * rpb, +rpb) of the backward, wave w taking rows w, w + 4, ... in groups of R rows
-// (R = 2 while a row's operands fit in registers twice): every load of a group (h, dy and dh of its
-// rows) is issued before the group's reductions, so one memory latency covers them. The dw partial of
-// the block (its 4 waves summed through LDS) goes to dw_part[blockIdx.x][N].
-template <int V, int MAXC, bool HAS_DELTA>
-__global__ __launch_bounds__(256) void add_rmsnorm_bwd_kernel(const char* __restrict__ dy, const char* __restrict__ dh,
-                                                              const char* __restrict__ h, const float* __restrict__ w,
-                                                              const float* __restrict__ rstd, char* __restrict__ dx,
-                                                              char* __restrict__ dd, float* __restrict__ dw_part,
-                                                              long long M, int N, long long rpb, int dydt, int hdt,
-                                                              int dxdt, int dddt) {
-    constexpr int R = V == 8 && MAXC <= 4 ? 2 : 1;  // as bwd_rows_per_group
-    __shared__ float red[2][MAXC * 64 * V];
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int chunks = N / V;
-    float wv[MAXC][V], dw[MAXC][V];
-#pragma unroll
-    for (int i = 0; i < MAXC; ++i) {
-        const int c = lane + 64 * i;
-        if (c < chunks) load<V>(reinterpret_cast<const char*>(w), (long long)c * V, kF32, wv[i]);
-#pragma unroll
-        for (int j = 0; j < V; ++j) dw[i][j] = 0.f;
-    }
-    const long long r0 = (long long)blockIdx.x * rpb;
-    const long long r1 = r0 + rpb < M ? r0 + rpb : M;
-    for (long long row0 = r0 + wave; row0 < r1; row0 += R * kRows) {
-        float n[R][MAXC][V], g[R][MAXC][V], res[R][MAXC][V];
-        bool live[R];
-#pragma unroll
-        for (int k = 0; k < R; ++k) {
-            const long long row = row0 + k * kRows;
-            live[k] = row < r1;
-            if (!live[k]) continue;
-#pragma unroll
-            for (int i = 0; i < MAXC; ++i) {
-                const int c = lane + 64 * i;
-                if (c >= chunks) break;
-                const long long off = row * N + (long long)c * V;
-                load<V>(h, off, hdt, n[k][i]);
-                load<V>(dy, off, dydt, g[k][i]);
-                if constexpr (HAS_DELTA) load<V>(dh, off, hdt, res[k][i]);
-            }
-        }
-#pragma unroll
-        for (int k = 0; k < R; ++k) {
-            if (!live[k]) continue;
-            const long long row = row0 + k * kRows;
-            const float r = rstd[row];
-            float dot = 0.f;
-#pragma unroll
-            for (int i = 0; i < MAXC; ++i) {
-                const int c = lane + 64 * i;
-                if (c >= chunks) break;
-#pragma unroll
-                for (int j = 0; j < V; ++j) {
-                    n[k][i][j] *= r;  // n = h * rstd
-                    dw[i][j] += g[k][i][j] * n[k][i][j];
-                    g[k][i][j] *= wv[i][j];  // dn = dy * w
-                    dot += g[k][i][j] * n[k][i][j];
-                }
-            }
-            const float mean = wave_sum(dot) / (float)N;
-#pragma unroll
-            for (int i = 0; i < MAXC; ++i) {
-                const int c = lane + 64 * i;
-                if (c >= chunks) break;
-                const long long off = row * N + (long long)c * V;
-                float o[V];
-#pragma unroll
-                for (int j = 0; j < V; ++j) {
-                    const float gj = (g[k][i][j] - n[k][i][j] * mean) * r;
-                    o[j] = HAS_DELTA ? res[k][i][j] + gj : gj;
-                }
-                store<V>(dx, off, dxdt, o);
-                if constexpr (HAS_DELTA) store<V>(dd, off, dddt, o);
-            }
-        }
-    }
-    // Waves 2, 3 hand their partials to waves 0, 1; wave 1 then hands the pair sum to wave 0.
-    if (wave >= 2) {
-#pragma unroll
-        for (int i = 0; i < MAXC; ++i)
-#pragma unroll
-            for (int j = 0; j < V; ++j) red[wave - 2][(i * 64 + lane) * V + j] = dw[i][j];
-    }
-    __syncthreads();
-    if (wave < 2) {
-#pragma unroll
-        for (int i = 0; i < MAXC; ++i)
-#pragma unroll
-            for (int j = 0; j < V; ++j) dw[i][j] += red[wave][(i * 64 + lane) * V + j];
-    }
-    __syncthreads();
-    if (wave == 1) {
-#pragma unroll
-        for (int i = 0; i < MAXC; ++i)
-#pragma unroll
-            for (int j = 0; j < V; ++j) red[0][(i * 64 + lane) * V + j] = dw[i][j];
-    }
-    __syncthreads();
-    if (wave == 0) {
-        float* out = dw_part + (long long)blockIdx.x * N;
-#pragma unroll
-        for (int i = 0; i < MAXC; ++i) {
-            const int c = lane + 64 * i;
-            if (c >= chunks) break;
-            float s[V];
-#pragma unroll
-            for (int j = 0; j < V; ++j) s[j] = dw[i][j] + red[0][(i * 64 + lane) * V + j];
-            store<V>(reinterpret_cast<char*>(out), (long long)c * V, kF32, s);
-        }
-    }
-}
-
-// Column sums of a [P][N] fp32 array over row slices: block (cb, sl) sums rows [sl * rps, +rps) of
-// columns cb * 64 .. +63 into out[sl][N]. Its 4 waves take every 4th row of the slice, each with 4
-// independent accumulators (so 4 loads are in flight per wave), and are then summed in wave order:
-// a fixed order, so the result is bit-reproducible. The backward's dw is two of these passes: the
-// per-block partials (at most 1024 rows) into slices of kSliceRows rows, then the slices into dw.
-constexpr int kSliceRows = 64;
-__global__ __launch_bounds__(256) void colsum_kernel(const float* __restrict__ part, float* __restrict__ out, int P,
-                                                     int N, int rps) {
-    __shared__ float red[kRows][64];
-    const int g = threadIdx.x >> 6, l = threadIdx.x & 63;
+// dw[c] = sum over p = 0 .. P-1 of part[p][c], in a fixed order: a block of 16 waves owns 64 columns;
+// wave v adds rows v, v + 16, ..., eight rows per step (eight loads in flight, summed pairwise), and the
+// 16 wave sums are then added in wave order. P = 0 writes zeros.
+__global__ __launch_bounds__(64 * kSumWaves) void colsum_kernel(const float* __restrict__ part,
+                                                                float* __restrict__ dw, int P, int N) {
+    __shared__ float red[kSumWaves][64];
+    const int v = threadIdx.x >> 6, l = threadIdx.x & 63;
     const int c = blockIdx.x * 64 + l;
-    const int p0 = blockIdx.y * rps;
-    const int p1 = p0 + rps < P ? p0 + rps : P;
-    float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+    float acc = 0.f;
     if (c < N) {
-        int p = p0 + g;
-        for (; p + 12 < p1; p += 16) {
-            a0 += part[(long long)p * N + c];
-            a1 += part[(long long)(p + 4) * N + c];
-            a2 += part[(long long)(p + 8) * N + c];
-            a3 += part[(long long)(p + 12) * N + c];
+        constexpr int U = 8, S = U * kSumWaves;
+        for (int p0 = v; p0 < P; p0 += S) {
+            float x[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int p = p0 + u * kSumWaves;
+                x[u] = p < P ? part[(long long)p * N + c] : 0.f;
+            }
+            acc += ((x[0] + x[1]) + (x[2] + x[3])) + ((x[4] + x[5]) + (x[6] + x[7]));
         }
-        for (; p < p1; p += 4) a0 += part[(long long)p * N + c];
     }
-    red[g][l] = (a0 + a1) + (a2 + a3);
+    red[v][l] = acc;
     __syncthreads();
-    if (g == 0 && c < N) out[(long long)blockIdx.y * N + c] = (red[0][l] + red[1][l]) + (red[2][l] + red[3][l]);
+    if (v == 0 && c < N) {
+        float s = 0.f;
+#pragma unroll
+        for (int m = 0; m < kSumWaves; ++m) s += red[m][l];
+        dw[c] = s;
+    }
 }
 
 // ------------------------------------------------------------------------------------------
@@ -333,49 +351,60 @@ bool aligned(const void* p, int a) { return ((uintptr_t)p & (uintptr_t)(a - 1)) 
 // The residual's dtype: fp32 if either is fp32 or they differ (fp16 + bf16), else their common type.
 int promote(int a, int b) { return a == b ? a : kF32; }
 
-// The shape variant: 16-byte chunks for N % 8 == 0 (up to 4096 elements, the reference's limit, where
-// the backward's row still fits in registers), single elements up to 1024.
-struct Shape {
-    int V, MAXC;
+// The team layout for a width: (W, R, K). 16-byte vectors (W = 8) when N is a multiple of 8 up to 4096;
+// single elements (W = 1, one 64-lane team, up to 16 per lane) for other widths up to 1024.
+struct Layout {
+    int W, R, K;
 };
-int pick_shape(long long N, Shape* s) {
-    if (N % 8 == 0 && N <= 4096) {
-        const int chunks = (int)(N / 8);
-        s->V = 8;
-        s->MAXC = chunks <= 128 ? 2 : chunks <= 256 ? 4 : 8;
+// The forward uses 64-lane teams up to 128 vectors as well (one row per wave, 2 vectors per lane at most):
+// measured faster than 32-lane teams for its single pass (14.6 against 14.8 us at 8192 x 768, 57.3 against
+// 61.5 us at 32768 x 768); the backward keeps 32-lane teams (two rows per wave, 3 vectors per lane at 768).
+int pick_layout(long long N, Layout* L, bool fwd = false) {
+    if (N % 8 == 0 && N >= 8 && N <= 4096) {
+        const int units = (int)(N / 8);
+        L->W = 8;
+        L->R = units <= 128 && !fwd ? 32 : 64;
+        const int k = (units + L->R - 1) / L->R;
+        L->K = L->R == 32 ? k : L->R == 64 && units <= 128 ? 2 : (k <= 4 ? 4 : k <= 6 ? 6 : 8);
         return 0;
     }
     if (N >= 1 && N <= 1024) {
-        s->V = 1;
-        s->MAXC = 16;
+        L->W = 1;
+        L->R = 64;
+        L->K = 16;
         return 0;
     }
     return fail("hidden size must be <= 1024, or a multiple of 8 and <= 4096; got %lld", N);
 }
 
-// Backward grid: R rows per wave and group (2 for N <= 2048, where a row group fits in registers),
-// a block's row range a multiple of 4R rows, at most kBwdBlocks blocks.
-int bwd_rows_per_group(long long N) { return N % 8 == 0 && N <= 2048 ? 2 : 1; }
-long long bwd_blocks(long long M, long long N) {
-    const long long per = kRows * bwd_rows_per_group(N);
-    const long long b = (M + per - 1) / per;
-    return b < kBwdBlocks ? b : kBwdBlocks;
+template <typename F>
+int with_layout(const Layout& L, bool delta, F&& f) {
+#define NNRMS_CASE(W_, R_, K_)                                                                    \
+    if (L.W == W_ && L.R == R_ && L.K == K_)                                                      \
+        return delta ? f(std::integral_constant<int, W_>{}, std::integral_constant<int, K_>{},    \
+                         std::integral_constant<int, R_>{}, std::true_type{})                     \
+                     : f(std::integral_constant<int, W_>{}, std::integral_constant<int, K_>{},    \
+                         std::integral_constant<int, R_>{}, std::false_type{});
+    NNRMS_CASE(8, 32, 1)
+    NNRMS_CASE(8, 32, 2)
+    NNRMS_CASE(8, 32, 3)
+    NNRMS_CASE(8, 32, 4)
+    NNRMS_CASE(8, 64, 2)
+    NNRMS_CASE(8, 64, 4)
+    NNRMS_CASE(8, 64, 6)
+    NNRMS_CASE(8, 64, 8)
+    NNRMS_CASE(1, 64, 16)
+#undef NNRMS_CASE
+    return fail("internal: no layout variant for W=%d R=%d K=%d", L.W, L.R, L.K);
 }
 
-template <typename F>
-int with_shape(const Shape& s, bool delta, F&& f) {
-#define NNRMS_CASE(V_, C_)                                                                     \
-    if (s.V == V_ && s.MAXC == C_)                                                             \
-        return delta ? f(std::integral_constant<int, V_>{}, std::integral_constant<int, C_>{}, \
-                         std::true_type{})                                                     \
-                     : f(std::integral_constant<int, V_>{}, std::integral_constant<int, C_>{}, \
-                         std::false_type{});
-    NNRMS_CASE(8, 2)
-    NNRMS_CASE(8, 4)
-    NNRMS_CASE(8, 8)
-    NNRMS_CASE(1, 16)
-#undef NNRMS_CASE
-    return fail("internal: no shape variant");
+long long rows_per_block(const Layout& L) { return 64LL * kWaves / L.R; }
+
+// Backward grid: enough blocks for one row per team, at most kBwdBlocks.
+long long bwd_blocks(long long M, const Layout& L) {
+    const long long per = 64LL * kBwdWaves / L.R;
+    const long long b = (M + per - 1) / per;
+    return b < kBwdBlocks ? b : kBwdBlocks;
 }
 
 }  // namespace
@@ -390,35 +419,30 @@ NNRMS_API int nn_add_rmsnorm_fwd(const void* x, const void* delta, const float* 
     if (!valid_dt(x_dtype) || !valid_dt(y_dtype) || (delta && !valid_dt(delta_dtype)))
         return fail("dtype must be float16, bfloat16 or float32");
     if (!(eps >= 0.f)) return fail("eps must be non-negative");
-    Shape s;
-    if (int e = pick_shape(N, &s)) return e;
+    Layout L;
+    if (int e = pick_layout(N, &L, true)) return e;
     if (M == 0) return 0;
     if (!x || !weight || !y || !rstd || (delta && !h)) return fail("null pointer argument");
     const int hdt = delta ? promote(x_dtype, delta_dtype) : x_dtype;
-    auto al = [&](const void* p, int dt) { return aligned(p, s.V == 8 ? 16 : elem_bytes(dt)); };
+    auto al = [&](const void* p, int dt) { return aligned(p, L.W == 8 ? 16 : elem_bytes(dt)); };
     if (!al(x, x_dtype) || !al(y, y_dtype) || !al(weight, kF32) || (delta && (!al(delta, delta_dtype) || !al(h, hdt))))
         return fail("tensors must be 16-byte aligned");
-    const long long blocks = (M + kRows - 1) / kRows;
+    const long long blocks = (M + rows_per_block(L) - 1) / rows_per_block(L);
     if (blocks >= (1LL << 31)) return fail("too many rows");
     hipStream_t st = (hipStream_t)stream;
-    return with_shape(s, delta != nullptr, [&](auto v, auto c, auto has_delta) {
-        add_rmsnorm_fwd_kernel<decltype(v)::value, decltype(c)::value, decltype(has_delta)::value>
-            <<<dim3((unsigned)blocks), dim3(256), 0, st>>>((const char*)x, (const char*)delta, weight, (char*)y,
-                                                           (char*)h, rstd, (long long)M, (int)N, eps, x_dtype,
-                                                           delta ? delta_dtype : x_dtype, hdt, y_dtype);
+    return with_layout(L, delta != nullptr, [&](auto w_, auto k_, auto r_, auto d_) {
+        add_rmsnorm_fwd_kernel<decltype(w_)::value, decltype(k_)::value, decltype(r_)::value, decltype(d_)::value>
+            <<<dim3((unsigned)blocks), dim3(64 * kWaves), 0, st>>>(x, delta, weight, y, h, rstd, (long long)M, (int)N,
+                                                                    eps, x_dtype, delta ? delta_dtype : x_dtype, hdt,
+                                                                    y_dtype);
         return launched("add_rmsnorm_fwd_kernel");
     });
 }
 
-// The dw reduction's passes: the per-block partial rows, and their slice sums when there are more than
-// one slice's worth.
-int dw_slices(long long P) { return P <= kSliceRows ? 1 : (int)((P + kSliceRows - 1) / kSliceRows); }
-
 NNRMS_API size_t nn_add_rmsnorm_bwd_workspace_size(int64_t M, int64_t N) {
-    if (M <= 0 || N <= 0) return 0;
-    const long long P = bwd_blocks(M, N);
-    const int S = dw_slices(P);
-    return (size_t)(P + (S > 1 ? S : 0)) * (size_t)N * 4;
+    Layout L;
+    if (M <= 0 || N <= 0 || pick_layout(N, &L)) return 0;
+    return (size_t)bwd_blocks(M, L) * (size_t)N * 4;
 }
 
 NNRMS_API int nn_add_rmsnorm_bwd(const void* dy, const void* dh, const void* h, const float* weight, const float* rstd,
@@ -428,45 +452,32 @@ NNRMS_API int nn_add_rmsnorm_bwd(const void* dy, const void* dh, const void* h, 
     if (M < 0 || N < 1) return fail("invalid sizes M=%lld N=%lld", (long long)M, (long long)N);
     if (!valid_dt(dy_dtype) || !valid_dt(h_dtype) || !valid_dt(dx_dtype) || (dh && !valid_dt(ddelta_dtype)))
         return fail("dtype must be float16, bfloat16 or float32");
-    Shape s;
-    if (int e = pick_shape(N, &s)) return e;
+    Layout L;
+    if (int e = pick_layout(N, &L)) return e;
     if (!dw || !weight) return fail("null pointer argument");
     hipStream_t st = (hipStream_t)stream;
-    if (M == 0) {  // no rows: dw = 0, written by the column sum over no partials (a kernel, not a memset)
-        colsum_kernel<<<dim3((unsigned)((N + 63) / 64), 1), dim3(256), 0, st>>>(nullptr, dw, 0, (int)N, 1);
+    const unsigned cblocks = (unsigned)((N + 63) / 64);
+    if (M == 0) {  // no rows: dw = 0, written by the column sum over no partial rows (a kernel, not a memset)
+        colsum_kernel<<<dim3(cblocks), dim3(64 * kSumWaves), 0, st>>>(nullptr, dw, 0, (int)N);
         return launched("colsum_kernel");
     }
     if (!dy || !h || !rstd || !dx || (dh && !ddelta)) return fail("null pointer argument");
     const size_t need = nn_add_rmsnorm_bwd_workspace_size(M, N);
     if (!workspace) return fail("null workspace");
     if (workspace_bytes < need) return fail("workspace too small: %zu bytes given, %zu needed", workspace_bytes, need);
-    auto al = [&](const void* p, int dt) { return aligned(p, s.V == 8 ? 16 : elem_bytes(dt)); };
-    if (!al(dy, dy_dtype) || !al(h, h_dtype) || !al(dx, dx_dtype) || !aligned(weight, s.V == 8 ? 16 : 4) ||
+    auto al = [&](const void* p, int dt) { return aligned(p, L.W == 8 ? 16 : elem_bytes(dt)); };
+    if (!al(dy, dy_dtype) || !al(h, h_dtype) || !al(dx, dx_dtype) || !aligned(weight, L.W == 8 ? 16 : 4) ||
         !aligned(workspace, 16) || !aligned(dw, 4) || (dh && (!al(dh, h_dtype) || !al(ddelta, ddelta_dtype))))
         return fail("tensors must be 16-byte aligned");
-    const long long P = bwd_blocks(M, N);
-    const long long per = kRows * bwd_rows_per_group(N);
-    const long long rpb = ((M + P - 1) / P + per - 1) / per * per;  // rows per block, a multiple of 4R
-    const long long P_used = (M + rpb - 1) / rpb;
-    int rc = with_shape(s, dh != nullptr, [&](auto v, auto c, auto has_delta) {
-        add_rmsnorm_bwd_kernel<decltype(v)::value, decltype(c)::value, decltype(has_delta)::value>
-            <<<dim3((unsigned)P_used), dim3(256), 0, st>>>((const char*)dy, (const char*)dh, (const char*)h, weight,
-                                                           rstd, (char*)dx, (char*)ddelta, (float*)workspace,
-                                                           (long long)M, (int)N, rpb, dy_dtype, h_dtype, dx_dtype,
-                                                           dh ? ddelta_dtype : dx_dtype);
+    const long long P = bwd_blocks(M, L);
+    int rc = with_layout(L, dh != nullptr, [&](auto w_, auto k_, auto r_, auto d_) {
+        add_rmsnorm_bwd_kernel<decltype(w_)::value, decltype(k_)::value, decltype(r_)::value, decltype(d_)::value>
+            <<<dim3((unsigned)P), dim3(64 * kBwdWaves), 0, st>>>(dy, dh, h, weight, rstd, dx, ddelta, (float*)workspace,
+                                                               (long long)M, (int)N, dy_dtype, h_dtype, dx_dtype,
+                                                               dh ? ddelta_dtype : dx_dtype);
         return launched("add_rmsnorm_bwd_kernel");
     });
     if (rc) return rc;
-    const unsigned cb = (unsigned)((N + 63) / 64);
-    const int S = dw_slices(P_used);
-    if (S == 1) {
-        colsum_kernel<<<dim3(cb, 1), dim3(256), 0, st>>>((const float*)workspace, dw, (int)P_used, (int)N, (int)P_used);
-        return launched("colsum_kernel");
-    }
-    float* slices = (float*)workspace + P_used * N;  // P_used <= P, so the slices fit where the size promised
-    colsum_kernel<<<dim3(cb, (unsigned)S), dim3(256), 0, st>>>((const float*)workspace, slices, (int)P_used, (int)N,
-                                                               kSliceRows);
-    if (int e = launched("colsum_kernel")) return e;
-    colsum_kernel<<<dim3(cb, 1), dim3(256), 0, st>>>(slices, dw, S, (int)N, S);
+    colsum_kernel<<<dim3(cblocks), dim3(64 * kSumWaves), 0, st>>>((const float*)workspace, dw, (int)P, (int)N);
     return launched("colsum_kernel");
 }

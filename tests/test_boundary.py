@@ -172,13 +172,14 @@ def test_rmsnorm_c_abi_rejects_bad_arguments_before_any_launch(kw, msg):
 
 def test_rmsnorm_c_abi_backward_checks_and_workspace():
     L = lib()
-    # one fp32 dw row per block (a block takes 8 rows, 2 per wave, for N <= 2048 with N % 8 == 0, else 4;
-    # at most 1024 blocks), plus one row per 64-row slice of those when there is more than one slice
-    assert L.nn_add_rmsnorm_bwd_workspace_size(8192, 768) == (1024 + 16) * 768 * 4
+    # one fp32 dw row per block of 8 waves: a block takes 16 rows per pass (32-lane teams) for N <= 1024 with
+    # N % 8 == 0, else 8 (64-lane teams); at most 512 blocks, whose teams then walk further rows
+    assert L.nn_add_rmsnorm_bwd_workspace_size(8192, 768) == 512 * 768 * 4
     assert L.nn_add_rmsnorm_bwd_workspace_size(7, 768) == 1 * 768 * 4
-    assert L.nn_add_rmsnorm_bwd_workspace_size(7, 4096) == 2 * 4096 * 4
-    assert L.nn_add_rmsnorm_bwd_workspace_size(520, 768) == (65 + 2) * 768 * 4
-    assert L.nn_add_rmsnorm_bwd_workspace_size(1 << 20, 33) == (1024 + 16) * 33 * 4
+    assert L.nn_add_rmsnorm_bwd_workspace_size(7, 4096) == 1 * 4096 * 4
+    assert L.nn_add_rmsnorm_bwd_workspace_size(520, 768) == 33 * 768 * 4
+    assert L.nn_add_rmsnorm_bwd_workspace_size(520, 2048) == 65 * 2048 * 4
+    assert L.nn_add_rmsnorm_bwd_workspace_size(1 << 20, 33) == 512 * 33 * 4
     assert L.nn_add_rmsnorm_bwd_workspace_size(0, 768) == 0
     args = (256, 512, 768, 1024, 2048, 4096, 8192, 16384)
     rc = L.nn_add_rmsnorm_bwd(*args, 32768, 10, 64, 768, 1, 2, 2, 1, None)
