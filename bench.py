@@ -110,6 +110,7 @@ def parse():
     p.add_argument("--heads", type=int, default=12)
     p.add_argument("--kv-heads", type=int, default=4)
     p.add_argument("--head-dim", type=int, default=64)
+    p.add_argument("--input-scale", type=float, default=1.0, help="q, k, v ~ N(0,1) times this (BASELINE config 3: 3.0)")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=16.0, help="budget of the CPU baseline sample (both forms)")
     p.add_argument("--profile-only", action="store_true", help="only the timed steps (for rocprofv3)")
@@ -328,9 +329,9 @@ def main():
     f_all = f_fwd + f_bwd
 
     torch.manual_seed(0)
-    q = torch.randn(B, H, T, D, device=dev).to(dtype)
-    k = torch.randn(B, KVH, T, D, device=dev).to(dtype)
-    v = torch.randn(B, KVH, T, D, device=dev).to(dtype)
+    q = (torch.randn(B, H, T, D, device=dev) * args.input_scale).to(dtype)
+    k = (torch.randn(B, KVH, T, D, device=dev) * args.input_scale).to(dtype)
+    v = (torch.randn(B, KVH, T, D, device=dev) * args.input_scale).to(dtype)
     do = torch.randn(B, H, T, D, device=dev).to(dtype)
 
     L = lib()
@@ -392,7 +393,8 @@ def main():
     for _ in range(args.warmup):
         step_abi()
         step_op()
-    flushed_op_steps(max(args.warmup, 3))
+    if not args.profile_only:
+        flushed_op_steps(max(args.warmup, 3))
     t_end = time.perf_counter() + args.prewarm
     while time.perf_counter() < t_end:
         for _ in range(200):  # the device never idles between these (the host runs ahead)
@@ -400,7 +402,9 @@ def main():
         torch.cuda.synchronize()
     # The headline: K steps through the torch.library ops, each after a cache flush, bracketed by device
     # synchronisations; value from the median step.
-    step_ms = flushed_op_steps(args.steps)
+    # (--profile-only: warm steps only, so that the per-kernel averages of a trace match the bench's own
+    # per-kernel event timings, which are taken on warm caches)
+    step_ms = flushed_op_steps(args.steps) if not args.profile_only else [float("nan")]
     ms = statistics.median(step_ms)
     # Beside it, warm-cache back-to-back steps: through the C ABI on resident outputs, and through the ops.
     abi_ms = timed(step_abi, args.steps)
@@ -493,6 +497,33 @@ def main():
         torch.cuda.synchronize()
     views_ms = timed(step_views, args.steps)
     fused_ms = timed(step_fused, args.steps)
+
+    # ---- q's RoPE folded into the attention: rope_qk + the layout-fused pair + rope_qk_bwd, against k's RoPE
+    # alone + the rope-fused pair + k's RoPE backward (the q tensor's trip through the RoPE kernels removed) ----
+    from nanonemo_amd.kernels.hip import rope as rp
+    from nanonemo_amd.model import rope_tables as _tables
+
+    cos_f, sin_f = (t.to(dev) for t in _tables(D, T, 10000.0))
+    q_empty = qp.new_empty(B, T, 0, D)
+
+    def step_rope_separate():
+        qr, kr = rp._rope_qk(qp, kp, cos_f, sin_f)
+        o2, lse2 = fa._flash_attn_bthd(qr, kr, vp)
+        dqr, dkr, dvr = fa._flash_attn_bthd_bwd(dop, qr, kr, vp, o2, lse2)
+        return rp._rope_qk_bwd(dqr, dkr, cos_f, sin_f), dvr
+
+    def step_rope_fused():
+        kr = rp._rope_qk(q_empty, kp, cos_f, sin_f)[1]
+        o2, lse2, qr = fa._flash_attn_bthd_rope(qp, kr, vp, cos_f, sin_f)
+        dq2, dkr, dvr = fa._flash_attn_bthd_rope_bwd(dop, qr, kr, vp, o2, lse2, cos_f, sin_f)
+        return dq2, rp._rope_qk_bwd(q_empty, dkr, cos_f, sin_f)[1], dvr
+
+    for _ in range(5):
+        step_rope_separate()
+        step_rope_fused()
+    rope_sep_ms = timed(step_rope_separate, args.steps)
+    rope_fused_ms = timed(step_rope_fused, args.steps)
+    qbytes = B * T * H * D * dtype.itemsize
 
     # ---- the RoPE kernel beside the op (q and k in the projection layout, one launch) ----
     from nanonemo_amd.kernels.hip.rope import rope_qk
@@ -607,7 +638,7 @@ def main():
             "workload": f"causal GQA attention fwd+bwd, B={B} T={T} {H}Q/{KVH}KV heads d={D} {args.dtype}: one "
             "nanonemo::flash_attn + nanonemo::flash_attn_bwd op pair per step on inputs resident in HBM, each step "
             "after a 512 MiB last-level-cache flush and timed alone with HIP events (median of the K steps)",
-            "B": B, "T": T, "H": H, "KVH": KVH, "D": D,
+            "B": B, "T": T, "H": H, "KVH": KVH, "D": D, "input_scale": args.input_scale,
         },
         "pct_of_bf16_peak": round(100 * value / PEAK_TFLOPS, 2),
         "step_ms": {
@@ -643,6 +674,17 @@ def main():
             "fwd_GBps": round(norm["fwd_bytes"] / (norm_us["fwd"] * 1e-6) / 1e9, 1),
             "bwd_us": round(norm_us["bwd"], 2),
             "bwd_GBps": round(norm["bwd_bytes"] / (norm_us["bwd"] * 1e-6) / 1e9, 1),
+        },
+        "rope_fusion": {
+            "how": "rope_qk(q, k) + flash_attn_bthd fwd + bwd + rope_qk_bwd(dq, dk), against rope of k alone + "
+            "flash_attn_bthd_rope fwd + bwd (q rotated in the forward's registers, dq rotated back in the dQ kernel) "
+            "+ rope_qk_bwd(dk); torch.library ops back to back, warm caches",
+            "separate_ms_per_step": round(rope_sep_ms, 5),
+            "fused_ms_per_step": round(rope_fused_ms, 5),
+            "saved_us": round((rope_sep_ms - rope_fused_ms) * 1e3, 2),
+            # the RoPE kernel's read of q (its q_rot write moves into the forward) and rope_qk_bwd's read and
+            # write of dq
+            "q_trip_bytes_removed": 3 * qbytes,
         },
         "layout_fusion": {
             "from": "projection layout (B, T, heads, hd)",

@@ -80,6 +80,34 @@ int nn_fa_bwd_strided(const void* dO, const void* q, const void* k, const void* 
                       const int64_t qo_strides[3], const int64_t kv_strides[3],
                       int dtype, float scale, void* stream);
 
+/* Forward with the rotary position embedding of q folded in: as nn_fa_fwd_strided, with q holding the
+ * projections *before* RoPE. Each query row is rotated in registers (rotate-half, dimension i paired with
+ * i + D/2, angle of the row's position: y[i] = x[i] cos - x[i+D/2] sin, y[i+D/2] = x[i] sin + x[i+D/2] cos,
+ * one fp32 rounding per product and sum, then one to the 16-bit type), used for the scores, and written to
+ * q_rot (q's layout) for the backward. cos_table / sin_table are dense fp32 [table_rows][D/2] with
+ * table_rows >= T, 16-byte aligned. k must already be rotated (nn_rope_qk with H = 0 rotates k alone).
+ * o, lse and q_rot are bit-identical to nn_rope_qk followed by nn_fa_fwd_strided. Replaces the q half of
+ * the RoPE call beside the op, /root/reference/nanonemo/model/layers.py:99-101 (apply_rope_qk of
+ * nanonemo/kernels/triton/rope.py), and the op's forward, flash_attn.py:18-22. */
+int nn_fa_fwd_rope_strided(const void* q, const void* k, const void* v, void* o, float* lse, void* q_rot,
+                           const float* cos_table, const float* sin_table, int64_t table_rows,
+                           int64_t B, int64_t H, int64_t KVH, int64_t T, int64_t D,
+                           const int64_t qo_strides[3], const int64_t kv_strides[3],
+                           int dtype, float scale, void* stream);
+
+/* Backward of nn_fa_fwd_rope_strided: as nn_fa_bwd_strided on q_rot, except that dq is the gradient of the
+ * *unrotated* q: the gradient reaching q_rot, rounded to the 16-bit type, rotated by -theta in the dQ kernel
+ * before its store. dk and dv are the gradients of the rotated k and of v. Bit-identical to
+ * nn_fa_bwd_strided followed by nn_rope_qk_bwd on dq. Replaces the op's backward (flash_attn.py:31-35) and
+ * the q half of RoPE's backward. */
+int nn_fa_bwd_rope_strided(const void* dO, const void* q_rot, const void* k, const void* v, const void* o,
+                           const float* lse, void* dq, void* dk, void* dv,
+                           void* workspace, size_t workspace_bytes,
+                           const float* cos_table, const float* sin_table, int64_t table_rows,
+                           int64_t B, int64_t H, int64_t KVH, int64_t T, int64_t D,
+                           const int64_t qo_strides[3], const int64_t kv_strides[3],
+                           int dtype, float scale, void* stream);
+
 /* Backward preprocessing alone: -D = -rowsum(dO * o) and -lse / scale, fp32, into the workspace.
  * Replaces the ATen preprocessing inside flash_bwd, flash_attn.cu:387-391. nn_fa_bwd does not call
  * it (nn_fa_bwd_dq performs the same pass in its prologue); it prepares the workspace for a caller

@@ -305,15 +305,39 @@ __device__ inline float pair_sum(float x) {
 __device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 __device__ inline float fast_log2(float x) { return __builtin_amdgcn_logf(x); }
 
+// Rotary position embedding folded into the attention (rotate-half, dimension i pairs with i + HD/2):
+//     y[i] = x[i] cos - x[i + HD/2] sin,   y[i + HD/2] = x[i] sin + x[i + HD/2] cos   at the row's position,
+// with one fp32 rounding per product and per sum (no contraction into fma) and one rounding to the 16-bit
+// type, so that it equals the standalone RoPE kernel's result bit for bit. The forward rotates its raw Q
+// rows and also writes them out (the backward's dK/dV kernel reads rotated Q); the dQ kernel applies the
+// inverse rotation (angle -theta) to its output. cos / sin are dense fp32 [table rows][HD/2] tables.
+struct RopeArgs {
+    const float* cosT;
+    const float* sinT;
+    u16* qrot;  // forward only: rotated Q, written with Q's layout
+};
+__device__ inline float mul_rn(float a, float b) {
+#pragma clang fp contract(off)
+    return a * b;
+}
+__device__ inline float add_rn(float a, float b) {
+#pragma clang fp contract(off)
+    return a + b;
+}
+__device__ inline float sub_rn(float a, float b) {
+#pragma clang fp contract(off)
+    return a - b;
+}
+
 // ------------------------------------------------------------------------------------------
 // Forward. Block = 4 waves = 128 query rows of one (batch, head); 128-key tiles of K and V,
 // double-buffered in LDS by DMA. Q stays in registers for the whole block.
 // ------------------------------------------------------------------------------------------
-template <int HD, int DT>
+template <int HD, int DT, bool ROPE>
 __global__ __launch_bounds__(256, 2) void fa_fwd_kernel(const u16* __restrict__ Q, const u16* __restrict__ K,
                                                         const u16* __restrict__ V, u16* __restrict__ O,
                                                         float* __restrict__ LSE, int BH, int H, int KVH, int T,
-                                                        int nqb, float sl2, Lay lq, Lay lk) {
+                                                        int nqb, float sl2, Lay lq, Lay lk, RopeArgs ra) {
     using E = Elem<DT>;
     constexpr int BM = 128, BN = 128, NW = 4;
     constexpr int NS = HD / 16;  // k-steps of Q K^T
@@ -343,6 +367,36 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_kernel(const u16* __restrict__ 
     u16x8 qf[NS];
 #pragma unroll
     for (int s = 0; s < NS; ++s) qf[s] = qrow < T ? ld8(Q + qoff + (size_t)qrow * lq.st + 16 * s + 8 * hh) : u16x8{};
+    if constexpr (ROPE) {
+        // qf[s] holds columns 16 s + 8 hh .. + 7 of the row, so qf[s] and qf[s + NS / 2] are the two halves of
+        // the same rotation pairs (columns c and c + HD / 2, c < HD / 2).
+        if (qrow < T) {
+            constexpr int HALF = HD / 2;
+            const float* cr = ra.cosT + (size_t)qrow * HALF;
+            const float* sr = ra.sinT + (size_t)qrow * HALF;
+#pragma unroll
+            for (int s = 0; s < NS / 2; ++s) {
+                const int c0 = 16 * s + 8 * hh;
+                const f32x4 ca = *reinterpret_cast<const f32x4*>(cr + c0), cb = *reinterpret_cast<const f32x4*>(cr + c0 + 4);
+                const f32x4 sa = *reinterpret_cast<const f32x4*>(sr + c0), sb = *reinterpret_cast<const f32x4*>(sr + c0 + 4);
+                float y1[8], y2[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const float cs = j < 4 ? ca[j] : cb[j - 4], sn = j < 4 ? sa[j] : sb[j - 4];
+                    const float x1 = E::to_f32(qf[s][j]), x2 = E::to_f32(qf[s + NS / 2][j]);
+                    y1[j] = sub_rn(mul_rn(x1, cs), mul_rn(x2, sn));
+                    y2[j] = add_rn(mul_rn(x1, sn), mul_rn(x2, cs));
+                }
+                const u32x4 w1 = {E::pack2(y1[0], y1[1]), E::pack2(y1[2], y1[3]), E::pack2(y1[4], y1[5]), E::pack2(y1[6], y1[7])};
+                const u32x4 w2 = {E::pack2(y2[0], y2[1]), E::pack2(y2[2], y2[3]), E::pack2(y2[4], y2[5]), E::pack2(y2[6], y2[7])};
+                qf[s] = __builtin_bit_cast(u16x8, w1);
+                qf[s + NS / 2] = __builtin_bit_cast(u16x8, w2);
+            }
+            u16* qo = ra.qrot + qoff + (size_t)qrow * lq.st;
+#pragma unroll
+            for (int s = 0; s < NS; ++s) *reinterpret_cast<u16x8*>(qo + 16 * s + 8 * hh) = qf[s];
+        }
+    }
 
     f32x16 oacc[ND];
 #pragma unroll
@@ -956,13 +1010,13 @@ __global__ __launch_bounds__(256) void fa_bwd_dkdv_sum_kernel(const float* __res
 //   dQ^T += K^T dS^T                    (A = columns of the K tile, B = dS^T registers)
 // dQ stays in registers for the whole key loop and is stored once, scaled, in the output dtype.
 // ------------------------------------------------------------------------------------------
-template <int HD, int DT>
+template <int HD, int DT, bool ROPE>
 __global__ __launch_bounds__(256, 2) void fa_bwd_dq_kernel(const u16* __restrict__ Q, const u16* __restrict__ K,
                                                            const u16* __restrict__ V, const u16* __restrict__ O,
                                                            const u16* __restrict__ dO, const float* __restrict__ LSE,
                                                            float* __restrict__ nLvec, float* __restrict__ nDvec,
                                                            u16* __restrict__ dQ, int BH, int H, int KVH, int T, int nqb,
-                                                           float sl2, float scale, Lay lq, Lay lk) {
+                                                           float sl2, float scale, Lay lq, Lay lk, RopeArgs ra) {
     using E = Elem<DT>;
     constexpr int BM = 128, BN = 64, NW = 4;
     constexpr int NS = HD / 16;
@@ -1102,14 +1156,49 @@ __global__ __launch_bounds__(256, 2) void fa_bwd_dq_kernel(const u16* __restrict
 
     if (qrow < T) {
         u16* dst = dQ + qoff + (size_t)qrow * lq.st;
+        if constexpr (ROPE) {
+            // The gradient reaching the rotated Q, rounded to the 16-bit type as a stored dQ would be, then the
+            // rotation by -theta. Element i of dq[dt] is column c = 32 dt + (i / 4) * 8 + 4 hh + i % 4; its pair
+            // (c + HD / 2) is element i of dq[1] (HD = 64) or element i + 8 of dq[0] (HD = 32).
+            constexpr int HALF = HD / 2;
+            const float* cr = ra.cosT + (size_t)qrow * HALF;
+            const float* sr = ra.sinT + (size_t)qrow * HALF;
+            float y[ND * 16];
 #pragma unroll
-        for (int dt = 0; dt < ND; ++dt)
+            for (int dt = 0; dt < ND; ++dt)
 #pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                const f32x16& a = dq[dt];
-                u32x2 w = {E::pack2(a[4 * g] * scale, a[4 * g + 1] * scale), E::pack2(a[4 * g + 2] * scale, a[4 * g + 3] * scale)};
-                *reinterpret_cast<u32x2*>(dst + 32 * dt + 8 * g + 4 * hh) = w;
+                for (int i = 0; i < 16; ++i) {
+                    const uint32_t w = E::pack2(dq[dt][i] * scale, 0.f);
+                    y[dt * 16 + i] = E::to_f32((u16)(w & 0xFFFFu));
+                }
+            // Groups g of 4 consecutive low-half columns c0 = 8 g + 4 hh .. + 3: elements 4 g .. 4 g + 3 of y, and
+            // their partners at y[16 + 4 g ..] (HD = 64, in dq[1]) or y[4 g + 8 ..] (HD = 32).
+#pragma unroll
+            for (int g = 0; g < ND * 2; ++g) {
+                const int c0 = 8 * g + 4 * hh;
+                const f32x4 cs = *reinterpret_cast<const f32x4*>(cr + c0), sn = *reinterpret_cast<const f32x4*>(sr + c0);
+                const int lo = 4 * g, hi = HD == 64 ? 16 + 4 * g : 4 * g + 8;
+                float r1[4], r2[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float y1 = y[lo + e], y2 = y[hi + e];
+                    r1[e] = add_rn(mul_rn(y1, cs[e]), mul_rn(y2, sn[e]));
+                    r2[e] = sub_rn(mul_rn(y2, cs[e]), mul_rn(y1, sn[e]));
+                }
+                const int clo = c0, chi = c0 + HALF;
+                *reinterpret_cast<u32x2*>(dst + clo) = u32x2{E::pack2(r1[0], r1[1]), E::pack2(r1[2], r1[3])};
+                *reinterpret_cast<u32x2*>(dst + chi) = u32x2{E::pack2(r2[0], r2[1]), E::pack2(r2[2], r2[3])};
             }
+        } else {
+#pragma unroll
+            for (int dt = 0; dt < ND; ++dt)
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const f32x16& a = dq[dt];
+                    u32x2 w = {E::pack2(a[4 * g] * scale, a[4 * g + 1] * scale), E::pack2(a[4 * g + 2] * scale, a[4 * g + 3] * scale)};
+                    *reinterpret_cast<u32x2*>(dst + 32 * dt + 8 * g + 4 * hh) = w;
+                }
+        }
     }
 }
 
@@ -1199,11 +1288,17 @@ Workspace carve(void* base, int64_t B, int64_t H, int64_t KVH, int64_t T, int64_
 
 template <int HD, int DT>
 int fwd_impl(const void* q, const void* k, const void* v, void* o, float* lse, int64_t B, int64_t H, int64_t KVH,
-             int64_t T, float scale, Lay lq, Lay lk, hipStream_t st) {
+             int64_t T, float scale, Lay lq, Lay lk, RopeArgs ra, hipStream_t st) {
     const int nqb = (int)((T + 127) / 128);
     const int BH = (int)(B * H);
-    fa_fwd_kernel<HD, DT><<<dim3(nqb * BH), dim3(256), 0, st>>>(
-        (const u16*)q, (const u16*)k, (const u16*)v, (u16*)o, lse, BH, (int)H, (int)KVH, (int)T, nqb, scale * kLog2e, lq, lk);
+    auto launch = [&](auto kern) {
+        kern<<<dim3(nqb * BH), dim3(256), 0, st>>>((const u16*)q, (const u16*)k, (const u16*)v, (u16*)o, lse, BH, (int)H,
+                                                   (int)KVH, (int)T, nqb, scale * kLog2e, lq, lk, ra);
+    };
+    if (ra.cosT)
+        launch(fa_fwd_kernel<HD, DT, true>);
+    else
+        launch(fa_fwd_kernel<HD, DT, false>);
     return launch_status("fa_fwd_kernel");
 }
 
@@ -1253,12 +1348,18 @@ int dkdv_impl(const void* q, const void* k, const void* v, const void* dO, const
 template <int HD, int DT>
 int dq_impl(const void* q, const void* k, const void* v, const void* o, const void* dO, const float* lse,
             const Workspace& w, void* dq, int64_t B, int64_t H, int64_t KVH, int64_t T, float scale, Lay lq, Lay lk,
-            hipStream_t st) {
+            RopeArgs ra, hipStream_t st) {
     const int nqb = (int)((T + 127) / 128);
     const int BH = (int)(B * H);
-    fa_bwd_dq_kernel<HD, DT><<<dim3(nqb * BH), dim3(256), 0, st>>>(
-        (const u16*)q, (const u16*)k, (const u16*)v, (const u16*)o, (const u16*)dO, lse, w.nL, w.nD, (u16*)dq, BH,
-        (int)H, (int)KVH, (int)T, nqb, scale * kLog2e, scale, lq, lk);
+    auto launch = [&](auto kern) {
+        kern<<<dim3(nqb * BH), dim3(256), 0, st>>>((const u16*)q, (const u16*)k, (const u16*)v, (const u16*)o,
+                                                   (const u16*)dO, lse, w.nL, w.nD, (u16*)dq, BH, (int)H, (int)KVH,
+                                                   (int)T, nqb, scale * kLog2e, scale, lq, lk, ra);
+    };
+    if (ra.cosT)
+        launch(fa_bwd_dq_kernel<HD, DT, true>);
+    else
+        launch(fa_bwd_dq_kernel<HD, DT, false>);
     return launch_status("fa_bwd_dq_kernel");
 }
 
@@ -1299,7 +1400,7 @@ int check_ws(void* workspace, size_t workspace_bytes, int64_t B, int64_t H, int6
 
 NNFA_API const char* nn_fa_last_error(void) { return g_last_error.c_str(); }
 
-NNFA_API int nn_fa_abi_version(void) { return 8; }
+NNFA_API int nn_fa_abi_version(void) { return 9; }
 
 NNFA_API size_t nn_fa_bwd_workspace_size(int64_t B, int64_t H, int64_t KVH, int64_t T, int64_t D) {
     if (B < 0 || H < 0 || KVH < 0 || T < 0 || D < 0) return 0;
@@ -1308,20 +1409,33 @@ NNFA_API size_t nn_fa_bwd_workspace_size(int64_t B, int64_t H, int64_t KVH, int6
 
 namespace {
 
+// The RoPE tables of the rope-fused entry points: non-null, 16-byte aligned, at least T rows.
+int check_rope(const float* cos_table, const float* sin_table, int64_t table_rows, int64_t T) {
+    if (!cos_table || !sin_table) return fail(-1, "null RoPE table");
+    if (((uintptr_t)cos_table & 15u) || ((uintptr_t)sin_table & 15u)) return fail(-1, "RoPE tables must be 16-byte aligned");
+    if (table_rows < T)
+        return fail(-1, "sequence length %lld exceeds the %lld rows of the RoPE tables", (long long)T, (long long)table_rows);
+    return 0;
+}
+
 int fwd_entry(const void* q, const void* k, const void* v, void* o, float* lse, int64_t B, int64_t H, int64_t KVH,
               int64_t T, int64_t D, int dtype, float scale, const int64_t* qo_strides, const int64_t* kv_strides,
-              void* stream) {
+              void* stream, RopeArgs ra = {}, int64_t table_rows = 0) {
     g_last_error.clear();
     if (int e = check_dims(B, H, KVH, T, D, dtype)) return e;
     if (B == 0 || T == 0) return 0;
     if (!q || !k || !v || !o || !lse) return fail(-1, "null pointer argument");
     if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o)) return fail(-1, "inputs must be 16-byte aligned");
+    if (ra.cosT || ra.sinT || ra.qrot) {
+        if (int e = check_rope(ra.cosT, ra.sinT, table_rows, T)) return e;
+        if (!ra.qrot || !aligned16(ra.qrot)) return fail(-1, "q_rot must be a 16-byte aligned buffer");
+    }
     Lay lq = contiguous(H, T, D), lk = contiguous(KVH, T, D);
     if (qo_strides)
         if (int e = take_layout(qo_strides, H, T, D, "q/o", &lq)) return e;
     if (kv_strides)
         if (int e = take_layout(kv_strides, KVH, T, D, "k/v", &lk)) return e;
-    return NNFA_DISPATCH(fwd_impl, D, dtype, q, k, v, o, lse, B, H, KVH, T, scale, lq, lk, (hipStream_t)stream);
+    return NNFA_DISPATCH(fwd_impl, D, dtype, q, k, v, o, lse, B, H, KVH, T, scale, lq, lk, ra, (hipStream_t)stream);
 }
 
 // Shared argument checks of the backward stages; fills the workspace view and the two layouts.
@@ -1370,7 +1484,8 @@ int dkdv_entry(const void* q, const void* k, const void* v, const void* dO, void
 
 int dq_entry(const void* q, const void* k, const void* v, const void* o, const void* dO, const float* lse,
              void* workspace, size_t workspace_bytes, void* dq, int64_t B, int64_t H, int64_t KVH, int64_t T,
-             int64_t D, int dtype, float scale, const int64_t* qo_strides, const int64_t* kv_strides, void* stream) {
+             int64_t D, int dtype, float scale, const int64_t* qo_strides, const int64_t* kv_strides, void* stream,
+             RopeArgs ra = {}, int64_t table_rows = 0) {
     Workspace w;
     Lay lq, lk;
     if (int e = bwd_prologue(workspace, workspace_bytes, B, H, KVH, T, D, dtype, qo_strides, kv_strides, &w, &lq, &lk))
@@ -1379,14 +1494,16 @@ int dq_entry(const void* q, const void* k, const void* v, const void* o, const v
     if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o) || !aligned16(dO) || !aligned16(dq))
         return fail(-1, "inputs must be 16-byte aligned");
     if (!(scale > 0.f)) return fail(-1, "scale must be positive");
-    return NNFA_DISPATCH(dq_impl, D, dtype, q, k, v, o, dO, lse, w, dq, B, H, KVH, T, scale, lq, lk,
+    if (ra.cosT || ra.sinT)
+        if (int e = check_rope(ra.cosT, ra.sinT, table_rows, T)) return e;
+    return NNFA_DISPATCH(dq_impl, D, dtype, q, k, v, o, dO, lse, w, dq, B, H, KVH, T, scale, lq, lk, ra,
                          (hipStream_t)stream);
 }
 
 int bwd_entry(const void* dO, const void* q, const void* k, const void* v, const void* o, const float* lse, void* dq,
               void* dk, void* dv, void* workspace, size_t workspace_bytes, int64_t B, int64_t H, int64_t KVH,
               int64_t T, int64_t D, int dtype, float scale, const int64_t* qo_strides, const int64_t* kv_strides,
-              void* stream) {
+              void* stream, RopeArgs ra = {}, int64_t table_rows = 0) {
     // Every argument of the three stages is checked before the first launch.
     Workspace w;
     Lay lq, lk;
@@ -1397,10 +1514,12 @@ int bwd_entry(const void* dO, const void* q, const void* k, const void* v, const
         !aligned16(dk) || !aligned16(dv))
         return fail(-1, "inputs must be 16-byte aligned");
     if (!(scale > 0.f)) return fail(-1, "scale must be positive");
+    if (ra.cosT || ra.sinT)
+        if (int e = check_rope(ra.cosT, ra.sinT, table_rows, T)) return e;
     // dQ first: it also computes -D and -lse/scale for its rows into the workspace (the preprocessing
     // pass, fused), which the dK/dV kernel reads.
     if (int e = dq_entry(q, k, v, o, dO, lse, workspace, workspace_bytes, dq, B, H, KVH, T, D, dtype, scale, qo_strides,
-                         kv_strides, stream))
+                         kv_strides, stream, ra, table_rows))
         return e;
     return dkdv_entry(q, k, v, dO, workspace, workspace_bytes, dk, dv, B, H, KVH, T, D, dtype, scale, qo_strides,
                       kv_strides, stream);
@@ -1454,6 +1573,29 @@ NNFA_API int nn_fa_bwd_strided(const void* dO, const void* q, const void* k, con
     if (!qo_strides || !kv_strides) return fail(-1, "null strides");
     return bwd_entry(dO, q, k, v, o, lse, dq, dk, dv, workspace, workspace_bytes, B, H, KVH, T, D, dtype, scale,
                      qo_strides, kv_strides, stream);
+}
+
+NNFA_API int nn_fa_fwd_rope_strided(const void* q, const void* k, const void* v, void* o, float* lse, void* q_rot,
+                                    const float* cos_table, const float* sin_table, int64_t table_rows, int64_t B,
+                                    int64_t H, int64_t KVH, int64_t T, int64_t D, const int64_t* qo_strides,
+                                    const int64_t* kv_strides, int dtype, float scale, void* stream) {
+    if (!qo_strides || !kv_strides) return fail(-1, "null strides");
+    const RopeArgs ra{cos_table, sin_table, (u16*)q_rot};
+    if (!cos_table || !sin_table || !q_rot) return fail(-1, "null RoPE table or q_rot");
+    return fwd_entry(q, k, v, o, lse, B, H, KVH, T, D, dtype, scale, qo_strides, kv_strides, stream, ra, table_rows);
+}
+
+NNFA_API int nn_fa_bwd_rope_strided(const void* dO, const void* q_rot, const void* k, const void* v, const void* o,
+                                    const float* lse, void* dq, void* dk, void* dv, void* workspace,
+                                    size_t workspace_bytes, const float* cos_table, const float* sin_table,
+                                    int64_t table_rows, int64_t B, int64_t H, int64_t KVH, int64_t T, int64_t D,
+                                    const int64_t* qo_strides, const int64_t* kv_strides, int dtype, float scale,
+                                    void* stream) {
+    if (!qo_strides || !kv_strides) return fail(-1, "null strides");
+    if (!cos_table || !sin_table) return fail(-1, "null RoPE table");
+    const RopeArgs ra{cos_table, sin_table, nullptr};
+    return bwd_entry(dO, q_rot, k, v, o, lse, dq, dk, dv, workspace, workspace_bytes, B, H, KVH, T, D, dtype, scale,
+                     qo_strides, kv_strides, stream, ra, table_rows);
 }
 
 // ------------------------------------------------------------------------------------------

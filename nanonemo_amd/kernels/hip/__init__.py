@@ -45,6 +45,15 @@ SIGNATURES: dict[str, tuple] = {
         [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _i64, _i64, _i64, _i64, _i64, _i64p, _i64p, _int, _f32,
          _vp],
     ),
+    "nn_fa_fwd_rope_strided": (
+        _int,
+        [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64p, _i64p, _int, _f32, _vp],
+    ),
+    "nn_fa_bwd_rope_strided": (
+        _int,
+        [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64p, _i64p,
+         _int, _f32, _vp],
+    ),
     "nn_fa_bwd_pre": (_int, [_vp, _vp, _vp, _vp, _sz, _i64, _i64, _i64, _i64, _i64, _int, _f32, _vp]),
     "nn_fa_bwd_dkdv": (_int, [_vp, _vp, _vp, _vp, _vp, _sz, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _int, _f32, _vp]),
     "nn_fa_bwd_dq": (
@@ -74,7 +83,7 @@ SIGNATURES: dict[str, tuple] = {
     "nn_rmsnorm_last_error": (ctypes.c_char_p, []),
 }
 
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 
 @cache

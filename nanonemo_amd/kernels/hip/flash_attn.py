@@ -234,3 +234,111 @@ def flash_attn_bthd(q: Tensor, k: Tensor, v: Tensor) -> Tensor:
     """Causal GQA attention in the projection layout: q (B, T, H, hd), k/v (B, T, KVH, hd) -> o (B, T, H, hd)."""
     o, _ = _flash_attn_bthd(q, k, v)
     return o
+
+
+# ---- RoPE of q folded into the layout-fused ops ------------------------------------------------
+# The reference rotates q and k beside the op (/root/reference/nanonemo/model/layers.py:99-101) and the op
+# then reads the rotated tensors. Here the forward takes q *before* RoPE, rotates each query row in registers
+# (the same fp32 operation order as nanonemo::rope_qk, so the result is bit-identical) and also returns the
+# rotated q, which the backward reads; the backward's dQ kernel rotates its gradient back by -theta before
+# storing it, so dq is the gradient of the unrotated q. k is rotated beforehand (rope_k). Not in the reference:
+# an addition the same model code can select (rope_kernel="fused"). The gradients of lse and of the rotated q
+# output are not propagated (the model uses neither), as the reference ignores lse's.
+
+
+def _check_tables(cos: Tensor, sin: Tensor, T: int, D: int) -> tuple[Tensor, Tensor]:
+    if cos.dtype != torch.float32 or sin.dtype != torch.float32 or cos.shape != sin.shape or cos.dim() != 2 \
+            or cos.shape[1] != D // 2 or cos.shape[0] < T or cos.device != sin.device:
+        raise RuntimeError("cos/sin must be float32 (T_max >= T, hd/2) tables on the inputs' device")
+    return _contig(cos), _contig(sin)
+
+
+@torch.library.custom_op("nanonemo::flash_attn_bthd_rope", mutates_args=())
+def _flash_attn_bthd_rope(q: Tensor, k: Tensor, v: Tensor, cos: Tensor, sin: Tensor) -> tuple[Tensor, Tensor, Tensor]:
+    q, k, v = _contig(q), _contig(k), _contig(v)
+    _check_inputs(q, k, v, seq_dim=1)
+    B, T, H, D = q.shape
+    KVH = k.size(2)
+    cos, sin = _check_tables(cos, sin, T, D)
+    o = torch.empty_like(q, memory_format=torch.contiguous_format)
+    q_rot = torch.empty_like(q, memory_format=torch.contiguous_format)
+    lse = torch.empty((B, H, T), dtype=torch.float32, device=q.device)
+    if B == 0 or T == 0 or H == 0:
+        return o, lse, q_rot
+    with torch.cuda.device(q.device):
+        rc = lib().nn_fa_fwd_rope_strided(
+            q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(), q_rot.data_ptr(),
+            cos.data_ptr(), sin.data_ptr(), cos.shape[0], B, H, KVH, T, D, _bthd_strides(q), _bthd_strides(k),
+            _DTYPES[q.dtype], 1.0 / math.sqrt(D), _stream(q),
+        )
+    check(rc)
+    return o, lse, q_rot
+
+
+@_flash_attn_bthd_rope.register_fake
+def _(q, k, v, cos, sin):
+    B, T, H, _ = q.shape
+    return (
+        torch.empty(q.shape, dtype=q.dtype, device=q.device),
+        torch.empty((B, H, T), dtype=torch.float32, device=q.device),
+        torch.empty(q.shape, dtype=q.dtype, device=q.device),
+    )
+
+
+@torch.library.custom_op("nanonemo::flash_attn_bthd_rope_bwd", mutates_args=())
+def _flash_attn_bthd_rope_bwd(
+    d_o: Tensor, q_rot: Tensor, k: Tensor, v: Tensor, o: Tensor, lse: Tensor, cos: Tensor, sin: Tensor
+) -> tuple[Tensor, Tensor, Tensor]:
+    d_o, q_rot, k, v, o, lse = (_contig(t) for t in (d_o, q_rot, k, v, o, lse))
+    _check_inputs(q_rot, k, v, seq_dim=1)
+    if d_o.shape != q_rot.shape or d_o.dtype != q_rot.dtype or o.shape != q_rot.shape or o.dtype != q_rot.dtype:
+        raise RuntimeError("d_o must be a contiguous float16/bfloat16 tensor shaped like q")
+    B, T, H, D = q_rot.shape
+    KVH = k.size(2)
+    if lse.shape != (B, H, T) or lse.dtype != torch.float32:
+        raise RuntimeError("lse must be a float32 tensor of shape (B, H, T)")
+    cos, sin = _check_tables(cos, sin, T, D)
+    dq = torch.empty_like(q_rot, memory_format=torch.contiguous_format)
+    dk = torch.empty_like(k, memory_format=torch.contiguous_format)
+    dv = torch.empty_like(v, memory_format=torch.contiguous_format)
+    if B == 0 or T == 0 or H == 0:
+        return dq, dk, dv
+    L = lib()
+    ws_bytes = L.nn_fa_bwd_workspace_size(B, H, KVH, T, D)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q_rot.device)
+    with torch.cuda.device(q_rot.device):
+        rc = L.nn_fa_bwd_rope_strided(
+            d_o.data_ptr(), q_rot.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(),
+            dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), ws.data_ptr(), ws_bytes, cos.data_ptr(), sin.data_ptr(),
+            cos.shape[0], B, H, KVH, T, D, _bthd_strides(q_rot), _bthd_strides(k), _DTYPES[q_rot.dtype],
+            1.0 / math.sqrt(D), _stream(q_rot),
+        )
+    check(rc)
+    return dq, dk, dv
+
+
+@_flash_attn_bthd_rope_bwd.register_fake
+def _(d_o, q_rot, k, v, o, lse, cos, sin):
+    return tuple(torch.empty(t.shape, dtype=t.dtype, device=t.device) for t in (q_rot, k, v))
+
+
+def _setup_context_rope(ctx, inputs, output):
+    _, k, v, cos, sin = inputs
+    o, lse, q_rot = output
+    ctx.save_for_backward(q_rot, k, v, o, lse, cos, sin)
+
+
+def _backward_rope(ctx, d_o, _d_lse, _d_q_rot):
+    q_rot, k, v, o, lse, cos, sin = ctx.saved_tensors
+    dq, dk, dv = _flash_attn_bthd_rope_bwd(d_o, q_rot, k, v, o, lse, cos, sin)
+    return dq, dk, dv, None, None
+
+
+_flash_attn_bthd_rope.register_autograd(_backward_rope, setup_context=_setup_context_rope)
+
+
+def flash_attn_bthd_rope(q: Tensor, k: Tensor, v: Tensor, cos: Tensor, sin: Tensor) -> Tensor:
+    """Causal GQA attention in the projection layout with q's RoPE folded in: q (B, T, H, hd) *before* RoPE,
+    k (B, T, KVH, hd) already rotated, v (B, T, KVH, hd), cos/sin fp32 (T_max, hd/2) -> o (B, T, H, hd)."""
+    o, _, _ = _flash_attn_bthd_rope(q, k, v, cos, sin)
+    return o

@@ -91,3 +91,9 @@ _rope_qk.register_autograd(_backward, setup_context=_setup_context)
 def rope_qk(q: Tensor, k: Tensor, cos: Tensor, sin: Tensor) -> tuple[Tensor, Tensor]:
     """Rotate q (B, T, H, hd) and k (B, T, KVH, hd) by the positions' angles (cos/sin: fp32 (T_max, hd/2))."""
     return _rope_qk(q, k, cos, sin)
+
+
+def rope_k(k: Tensor, cos: Tensor, sin: Tensor) -> Tensor:
+    """Rotate k (B, T, KVH, hd) alone (the q half of the pass is folded into the attention op)."""
+    q = k.new_empty(k.shape[0], k.shape[1], 0, k.shape[3])
+    return _rope_qk(q, k, cos, sin)[1]

@@ -13,7 +13,8 @@ tied input/output embedding, GPT-2 style init with the residual projections scal
              "cuda" setting, layers.py:89-93,106-108, including its transposes and copies);
   * "hip_bthd": the layout-fused op nanonemo::flash_attn_bthd, which reads the projections and RoPE
              output in their (B, T, heads, hd) layout and writes o where the output projection reads it.
-``rope_kernel="hip"`` rotates q and k with this build's RoPE kernel (nanonemo::rope_qk) and
+``rope_kernel="hip"`` rotates q and k with this build's RoPE kernel (nanonemo::rope_qk), ``rope_kernel="fused"``
+rotates k with it and q inside the layout-fused attention op (nanonemo::flash_attn_bthd_rope), and
 ``norm_kernel="hip"`` runs the residual add + RMSNorm on either side of attention as this build's fused
 kernel (nanonemo::cuda_add_rms_norm_fwd / _bwd, the reference's norm_kernel="cuda"); everything else
 is plain PyTorch.
@@ -50,7 +51,9 @@ class ModelConfig:
     # batched products on transposed operands, which the math backend's forward and backward make)
     attn_backend: str = "math"
     attn_kernel: str = "torch"  # "torch" | "hip" | "hip_bthd"
-    rope_kernel: str = "torch"  # "torch" | "hip" (q and k rotated in one launch, nanonemo::rope_qk)
+    # "torch" | "hip" (q and k rotated in one launch, nanonemo::rope_qk) | "fused" (q rotated inside the attention
+    # op nanonemo::flash_attn_bthd_rope, k alone by nanonemo::rope_qk; needs attn_kernel="hip_bthd")
+    rope_kernel: str = "torch"
     norm_kernel: str = "torch"  # "torch" | "hip" (fused residual add + RMSNorm, nanonemo::cuda_add_rms_norm_*)
 
     def __post_init__(self):
@@ -64,8 +67,10 @@ class ModelConfig:
             raise ValueError(f"unknown attn_backend {self.attn_backend!r}")
         if self.attn_kernel not in ("torch", "hip", "hip_bthd"):
             raise ValueError(f"unknown attn_kernel {self.attn_kernel!r}")
-        if self.rope_kernel not in ("torch", "hip"):
+        if self.rope_kernel not in ("torch", "hip", "fused"):
             raise ValueError(f"unknown rope_kernel {self.rope_kernel!r}")
+        if self.rope_kernel == "fused" and self.attn_kernel != "hip_bthd":
+            raise ValueError('rope_kernel="fused" needs attn_kernel="hip_bthd"')
         if self.norm_kernel not in ("torch", "hip"):
             raise ValueError(f"unknown norm_kernel {self.norm_kernel!r}")
 
@@ -143,16 +148,19 @@ class Attention(nn.Module):
             from nanonemo_amd.kernels.hip import flash_attn as fa  # registers the ops; raises without the library
 
             self._fa = fa
-        if cfg.rope_kernel == "hip":
-            from nanonemo_amd.kernels.hip.rope import rope_qk
+        if cfg.rope_kernel in ("hip", "fused"):
+            from nanonemo_amd.kernels.hip.rope import rope_k, rope_qk
 
-            self._rope_qk = rope_qk
+            self._rope_qk, self._rope_k = rope_qk, rope_k
 
     def forward(self, x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
         B, T, _ = x.shape
         q = self.wq(x).view(B, T, self.H, self.hd)
         k = self.wk(x).view(B, T, self.KVH, self.hd)
         v = self.wv(x).view(B, T, self.KVH, self.hd)
+        if self.cfg.rope_kernel == "fused":  # k rotated here, q inside the attention op
+            k = self._rope_k(k, cos, sin)
+            return self.wo(self._fa.flash_attn_bthd_rope(q, k, v, cos, sin).view(B, T, -1))
         hip_rope = self.cfg.rope_kernel == "hip"
         if hip_rope:  # in the projection layout, q and k in one launch
             q, k = self._rope_qk(q, k, cos, sin)

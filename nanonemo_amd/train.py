@@ -73,13 +73,15 @@ def make_optimizer(model, lr: float = 6e-4):
 def run(attn: str, steps: int, batch: int, seq: int, cfg_kwargs: dict, device: str = "cuda", warmup: int = 3):
     """Train ``steps`` steps from the seed-0 init on the seed-0 synthetic stream; returns the per-step
     losses and the tokens/s over the steps after ``warmup``. ``attn`` is an attn_kernel, optionally
-    with "+rope" (rope_kernel="hip") and "+norm" (norm_kernel="hip") suffixes."""
+    with "+rope" (rope_kernel="hip"), "+qrope" (rope_kernel="fused": q's RoPE inside the attention op)
+    and "+norm" (norm_kernel="hip") suffixes."""
     torch.manual_seed(0)
     kernel, *extras = attn.split("+")
-    unknown = set(extras) - {"rope", "norm"}
+    unknown = set(extras) - {"rope", "qrope", "norm"}
     if unknown:
         raise ValueError(f"unknown kernel suffixes {sorted(unknown)}")
-    model = NanoNemo(ModelConfig(**cfg_kwargs, attn_kernel=kernel, rope_kernel="hip" if "rope" in extras else "torch",
+    rope = "fused" if "qrope" in extras else "hip" if "rope" in extras else "torch"
+    model = NanoNemo(ModelConfig(**cfg_kwargs, attn_kernel=kernel, rope_kernel=rope,
                                  norm_kernel="hip" if "norm" in extras else "torch")).to(device)
     opt = make_optimizer(model)
     data = synthetic_batches(steps, batch, seq, model.cfg.vocab_size, device)
@@ -102,8 +104,10 @@ def main():
     p.add_argument("--steps", type=int, default=50)
     p.add_argument("--batch", type=int, default=8)
     p.add_argument("--seq", type=int, default=1024)
-    p.add_argument("--attn", nargs="+", default=["torch", "hip", "hip_bthd", "hip_bthd+rope", "hip_bthd+rope+norm"],
-                   help="attention kernels; '+rope' / '+norm' suffixes also select the HIP RoPE / add+RMSNorm kernels")
+    p.add_argument("--attn", nargs="+",
+                   default=["torch", "hip", "hip_bthd", "hip_bthd+rope", "hip_bthd+rope+norm", "hip_bthd+qrope+norm"],
+                   help="attention kernels; '+rope' / '+qrope' / '+norm' suffixes also select the HIP RoPE (separate / "
+                   "q folded into the attention) and add+RMSNorm kernels")
     p.add_argument("--small", action="store_true", help="a 2-layer model (quick check)")
     p.add_argument("--torch-backend", default="math_fp32", choices=["math", "mem_efficient", "math_fp32"],
                    help="SDPA backend of the torch attention (math_fp32: fp32 math on upcast q, k, v)")

@@ -267,6 +267,41 @@ def test_layout_fused_fakes_keep_the_projection_layout():
     assert fa.flash_attn_bthd(q, k, k).view(B, T, H * D).shape == (B, T, H * D)
 
 
+def test_rope_fused_ops_registered_and_faked():
+    fa = _ops()
+    fwd = str(torch.ops.nanonemo.flash_attn_bthd_rope.default._schema)
+    bwd = str(torch.ops.nanonemo.flash_attn_bthd_rope_bwd.default._schema)
+    assert fwd == "nanonemo::flash_attn_bthd_rope(Tensor q, Tensor k, Tensor v, Tensor cos, Tensor sin) -> (Tensor, Tensor, Tensor)"
+    assert bwd == ("nanonemo::flash_attn_bthd_rope_bwd(Tensor d_o, Tensor q_rot, Tensor k, Tensor v, Tensor o, Tensor lse, "
+                   "Tensor cos, Tensor sin) -> (Tensor, Tensor, Tensor)")
+    B, T, H, KVH, D = 2, 64, 12, 4, 64
+    q = torch.empty(B, T, H, D, dtype=torch.bfloat16, device="meta")
+    k = torch.empty(B, T, KVH, D, dtype=torch.bfloat16, device="meta")
+    cos = torch.empty(T, D // 2, device="meta")
+    o, lse, q_rot = torch.ops.nanonemo.flash_attn_bthd_rope(q, k, k, cos, cos)
+    assert o.shape == q_rot.shape == q.shape and o.is_contiguous() and lse.shape == (B, H, T)
+    dq, dk, dv = torch.ops.nanonemo.flash_attn_bthd_rope_bwd(o, q_rot, k, k, o, lse, cos, cos)
+    assert dq.shape == q.shape and dk.shape == k.shape and dv.shape == k.shape
+    assert fa.flash_attn_bthd_rope(q, k, k, cos, cos).shape == q.shape
+
+
+def test_rope_fused_c_abi_checks_tables_before_any_launch():
+    L = lib()
+    s3 = (ctypes.c_int64 * 3)(1024 * 12 * 64, 64, 12 * 64)
+    k3 = (ctypes.c_int64 * 3)(1024 * 4 * 64, 64, 4 * 64)
+    args = (256, 512, 768, 1024, 2048, 4096)
+    rc = L.nn_fa_fwd_rope_strided(*args, None, 8192, 1024, 1, 12, 4, 1024, 64, s3, k3, 1, 0.125, None)
+    assert rc != 0 and b"null RoPE table" in L.nn_fa_last_error()
+    rc = L.nn_fa_fwd_rope_strided(*args, 8192, 16384, 512, 1, 12, 4, 1024, 64, s3, k3, 1, 0.125, None)
+    assert rc != 0 and b"exceeds the 512 rows" in L.nn_fa_last_error()
+    rc = L.nn_fa_fwd_rope_strided(*args, 8200, 16384, 1024, 1, 12, 4, 1024, 64, s3, k3, 1, 0.125, None)
+    assert rc != 0 and b"16-byte aligned" in L.nn_fa_last_error()
+    ws = L.nn_fa_bwd_workspace_size(1, 12, 4, 1024, 64)
+    rc = L.nn_fa_bwd_rope_strided(*args, 256, 512, 768, 256, ws, 8192, 16384, 1000, 1, 12, 4, 1024, 64, s3, k3, 1,
+                                  0.125, None)
+    assert rc != 0 and b"exceeds the 1000 rows" in L.nn_fa_last_error()
+
+
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 def test_fake_impls_give_contiguous_outputs_for_strided_inputs(dtype):
     fa = _ops()
