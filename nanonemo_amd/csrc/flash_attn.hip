@@ -1003,8 +1003,8 @@ __global__ __launch_bounds__(256) void fa_bwd_dkdv_sum_kernel(const float* __res
 
 // ------------------------------------------------------------------------------------------
 // Backward, dQ. Shaped like the forward: block = 4 waves = 128 query rows of one (batch, head),
-// 64-key tiles of K and V double-buffered in LDS by DMA, Q and dO rows in registers, lse and D
-// per lane. Per tile:
+// 128-key tiles of K and V double-buffered in LDS by DMA and processed in 64-key halves, Q and dO rows
+// in registers, lse and D per lane. Per 64-key half:
 //   S^T = K Q^T, dP^T = V dO^T          (A = K / V rows from LDS, B = Q / dO registers)
 //   dS^T = exp2((S^T - lse/scale) * sl2) (dP^T - D)
 //   dQ^T += K^T dS^T                    (A = columns of the K tile, B = dS^T registers)
@@ -1018,11 +1018,13 @@ __global__ __launch_bounds__(256, 2) void fa_bwd_dq_kernel(const u16* __restrict
                                                            u16* __restrict__ dQ, int BH, int H, int KVH, int T, int nqb,
                                                            float sl2, float scale, Lay lq, Lay lk, RopeArgs ra) {
     using E = Elem<DT>;
-    constexpr int BM = 128, BN = 64, NW = 4;
+    // LDS tiles of BT = 128 keys (one barrier and one tile wait per 128 keys), each processed as two BN = 64-key
+    // halves (the register working set of a 64-key step).
+    constexpr int BM = 128, BN = 64, NW = 4, BT = 128;
     constexpr int NS = HD / 16;
     constexpr int ND = HD / 32;
     constexpr int NT = BN / 32;
-    constexpr int TILE = BN * HD;
+    constexpr int TILE = BT * HD;
     __shared__ __attribute__((aligned(16))) u16 kA[TILE];
     __shared__ __attribute__((aligned(16))) u16 vA[TILE];
     __shared__ __attribute__((aligned(16))) u16 kB[TILE];
@@ -1039,7 +1041,7 @@ __global__ __launch_bounds__(256, 2) void fa_bwd_dq_kernel(const u16* __restrict
 
     const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const DmaOffs<HD, BN, NW> dfo = dma_offsets<HD, BN, NW>(lane, wave, lk.st);
+    const DmaOffs<HD, BT, NW> dfo = dma_offsets<HD, BT, NW>(lane, wave, lk.st);
     const int g16 = (lane >> 4) & 1;
     const int q0 = qb * BM, qw = q0 + wave * 32, qrow = qw + l32;
     const int qc_ = min(qrow, T - 1);
@@ -1077,10 +1079,10 @@ __global__ __launch_bounds__(256, 2) void fa_bwd_dq_kernel(const u16* __restrict
 #pragma unroll
     for (int dt = 0; dt < ND; ++dt) dq[dt] = f32x16{};
 
-    const int ntiles = (min(q0 + BM, T) + BN - 1) / BN;
+    const int ntiles = (min(q0 + BM, T) + BT - 1) / BT;
     auto issue = [&](int it, u16* kb, u16* vb) {
-        dma_rows<HD, BN, NW>(Kp, lk.st, it * BN, T, kb, wave, dfo);
-        dma_rows<HD, BN, NW>(Vp, lk.st, it * BN, T, vb, wave, dfo);
+        dma_rows<HD, BT, NW>(Kp, lk.st, it * BT, T, kb, wave, dfo);
+        dma_rows<HD, BT, NW>(Vp, lk.st, it * BT, T, vb, wave, dfo);
     };
     // -D enters as the initial value of every dP^T accumulator (the same for all of a lane's keys).
     f32x16 ndv;
@@ -1088,7 +1090,7 @@ __global__ __launch_bounds__(256, 2) void fa_bwd_dq_kernel(const u16* __restrict
     for (int i = 0; i < 16; ++i) ndv[i] = nd;
     // MASK: the tile crosses the diagonal or T (a separate instantiation, so that unmasked tiles
     // carry no per-element selects).
-    auto tile = [&](auto mask_tag, int k0, const u16* kb, const u16* vb) {
+    auto tile = [&](auto mask_tag, int k0, const u16* kb, const u16* vb) __attribute__((always_inline)) {
         constexpr bool MASK = decltype(mask_tag)::value;
         u16x8 ka[NT][NS], va[NT][NS];
 #pragma unroll
@@ -1132,13 +1134,16 @@ __global__ __launch_bounds__(256, 2) void fa_bwd_dq_kernel(const u16* __restrict
                 dq[dt] = E::mfma(cat4(ld_tr(kc + kcol[dt][0]), ld_tr(kc + kcol[dt][1])), sf, dq[dt]);
         }
     };
-    auto step = [&](int it, const u16* kb, const u16* vb) {
-        const int k0 = it * BN;
-        if (qw >= T || k0 > qw + 31) return;  // no visible key in this tile for this wave
+    auto half = [&](int k0, const u16* kb, const u16* vb) __attribute__((always_inline)) {
+        if (qw >= T || k0 > qw + 31) return;  // no visible key in this half for this wave
         if (k0 + BN - 1 > qw || k0 + BN > T)
             tile(std::true_type{}, k0, kb, vb);
         else
             tile(std::false_type{}, k0, kb, vb);
+    };
+    auto step = [&](int it, const u16* kb, const u16* vb) __attribute__((always_inline)) {
+        half(it * BT, kb, vb);
+        half(it * BT + BN, kb + BN * HD, vb + BN * HD);
     };
 
     issue(0, kA, vA);
