@@ -52,7 +52,7 @@ typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 
 constexpr int kF16 = 0, kBF16 = 1, kF32 = 2;
 constexpr int kWaves = 4;         // waves per block of the forward
-constexpr int kBwdWaves = 8;      // waves per block of the backward
+constexpr int kBwdWaves = 8;      // waves per block of the backward (4 for the widest rows, see bwd_waves)
 constexpr int kBwdBlocks = 512;   // most blocks of the backward (each then owns one dw partial row)
 constexpr int kSumWaves = 16;     // waves of a column-sum block
 
@@ -218,74 +218,137 @@ __global__ __launch_bounds__(64 * kWaves) void add_rmsnorm_fwd_kernel(const void
 // teams of a wave are summed over their lane groups and the block's waves in LDS into partial row
 // blockIdx.x.
 // ------------------------------------------------------------------------------------------
-template <int W, int K, int R, bool DELTA>
-__global__ __launch_bounds__(64 * kBwdWaves) void add_rmsnorm_bwd_kernel(
+template <int W, int K, int R, bool DELTA, int NWV>
+__global__ __launch_bounds__(64 * NWV) void add_rmsnorm_bwd_kernel(
     const void* __restrict__ dy, const void* __restrict__ dh, const void* __restrict__ h, const float* __restrict__ w,
     const float* __restrict__ rstd, void* __restrict__ dx, void* __restrict__ ddelta, float* __restrict__ dw_part,
     long long M, int N, int dydt, int hdt, int dxdt, int dddt) {
-    constexpr int TPB = 64 * kBwdWaves / R;
-    __shared__ float red[kBwdWaves][K * R * W];  // each wave's dw, unit-major per lane position
+    constexpr int TPB = 64 * NWV / R;
+    // Wide rows (more than 32 values per lane) take two passes over the row per team: the first sums g * h and
+    // dw, the second re-reads the row (now in cache) for dx, so that only dw stays resident across rows.
+    constexpr bool TWO_PASS = W * K > 32;
+    __shared__ float red[NWV][R * W];  // one unit's dw per wave, per lane position
     const int team = threadIdx.x / R, t = threadIdx.x % R, wave = threadIdx.x >> 6;
     const int units = N / W;
     const long long teams = (long long)gridDim.x * TPB;
     const int dyb = elem_bytes(dydt), hb = elem_bytes(hdt);
 
     Slice<W, K> wv, acc;
-    load_weight<W, K, R>(w, t, units, wv);
+    if constexpr (!TWO_PASS) load_weight<W, K, R>(w, t, units, wv);
 #pragma unroll
     for (int k = 0; k < K; ++k)
 #pragma unroll
         for (int e = 0; e < W; ++e) acc.v[k][e] = 0.f;
 
+    // Unit k of this lane of tensor p (dtype dt) at row offset off, widened to fp32 (zeros past the row).
+    auto unit = [&](const void* p, int dt, long long off, int k, float* v) {
+        const int u = t + k * R;
+        if constexpr (W == 8) {
+            const f32x8 x = u < units ? load_vec((const char*)p + off * elem_bytes(dt), u, dt) : f32x8{};
+#pragma unroll
+            for (int e = 0; e < 8; ++e) v[e] = x[e];
+        } else {
+            v[0] = u < units ? load_one((const char*)p + off * elem_bytes(dt), u, dt) : 0.f;
+        }
+    };
+
     for (long long row = (long long)blockIdx.x * TPB + team; row < M; row += teams) {
         const long long off = row * N;
-        Slice<W, K> gv, hv, res;  // dy (then g, then the gradient), h, and dh
-        load_slice<W, K, R>((const char*)dy + off * dyb, dydt, t, units, gv);
-        load_slice<W, K, R>((const char*)h + off * hb, hdt, t, units, hv);
-        if constexpr (DELTA) load_slice<W, K, R>((const char*)dh + off * hb, hdt, t, units, res);
         const float r = rstd[row];
-        float s = 0.f;
+        if constexpr (TWO_PASS) {
+            float s = 0.f;
 #pragma unroll
-        for (int k = 0; k < K; ++k)
+            for (int k = 0; k < K; ++k) {
+                float g[W], hv[W], wk[W];
+                unit(dy, dydt, off, k, g);
+                unit(h, hdt, off, k, hv);
+                unit(w, kF32, 0, k, wk);
 #pragma unroll
-            for (int e = 0; e < W; ++e) {
-                acc.v[k][e] = fmaf(gv.v[k][e], hv.v[k][e] * r, acc.v[k][e]);  // dw += dy * (h r)
-                gv.v[k][e] *= wv.v[k][e];                                     // g = dy * w
-                s = fmaf(gv.v[k][e], hv.v[k][e], s);
+                for (int e = 0; e < W; ++e) {
+                    acc.v[k][e] = fmaf(g[e], hv[e] * r, acc.v[k][e]);  // dw += dy * (h r)
+                    s = fmaf(g[e] * wk[e], hv[e], s);                   // g = dy * w
+                }
+                __builtin_amdgcn_sched_barrier(0);  // keep each unit's loads next to their use (registers)
             }
-        const float c = r * r * r * team_sum<R>(s) / (float)N;
+            const float c = r * r * r * team_sum<R>(s) / (float)N;
+            // the second pass re-reads the row from cache: without this the compiler keeps the first pass's loaded
+            // values live instead (the same addresses), which is what this form avoids
+            __asm__ volatile("" ::: "memory");
 #pragma unroll
-        for (int k = 0; k < K; ++k)
+            for (int k = 0; k < K; ++k) {
+                const int u = t + k * R;
+                if (u >= units) continue;
+                float g[W], hv[W], wk[W], res[W];
+                unit(dy, dydt, off, k, g);
+                unit(h, hdt, off, k, hv);
+                unit(w, kF32, 0, k, wk);
+                if constexpr (DELTA) unit(dh, hdt, off, k, res);
+                f32x8 d8;
 #pragma unroll
-            for (int e = 0; e < W; ++e) {
-                const float d = gv.v[k][e] * r - hv.v[k][e] * c;
-                gv.v[k][e] = DELTA ? d + res.v[k][e] : d;
+                for (int e = 0; e < W; ++e) {
+                    const float d = (g[e] * wk[e]) * r - hv[e] * c;
+                    g[e] = DELTA ? d + res[e] : d;
+                    if constexpr (W == 8) d8[e] = g[e];
+                }
+                if constexpr (W == 8) {
+                    store_vec((char*)dx + off * elem_bytes(dxdt), u, dxdt, d8);
+                    if constexpr (DELTA) store_vec((char*)ddelta + off * elem_bytes(dddt), u, dddt, d8);
+                } else {
+                    store_one((char*)dx + off * elem_bytes(dxdt), u, dxdt, g[0]);
+                    if constexpr (DELTA) store_one((char*)ddelta + off * elem_bytes(dddt), u, dddt, g[0]);
+                }
+                __builtin_amdgcn_sched_barrier(0);
             }
-        store_slice<W, K, R>((char*)dx + off * elem_bytes(dxdt), dxdt, t, units, gv);
-        if constexpr (DELTA) store_slice<W, K, R>((char*)ddelta + off * elem_bytes(dddt), dddt, t, units, gv);
+        } else {
+            Slice<W, K> gv, hv, res;  // dy (then g, then the gradient), h, and dh
+            load_slice<W, K, R>((const char*)dy + off * dyb, dydt, t, units, gv);
+            load_slice<W, K, R>((const char*)h + off * hb, hdt, t, units, hv);
+            if constexpr (DELTA) load_slice<W, K, R>((const char*)dh + off * hb, hdt, t, units, res);
+            float s = 0.f;
+#pragma unroll
+            for (int k = 0; k < K; ++k)
+#pragma unroll
+                for (int e = 0; e < W; ++e) {
+                    acc.v[k][e] = fmaf(gv.v[k][e], hv.v[k][e] * r, acc.v[k][e]);  // dw += dy * (h r)
+                    gv.v[k][e] *= wv.v[k][e];                                     // g = dy * w
+                    s = fmaf(gv.v[k][e], hv.v[k][e], s);
+                }
+            const float c = r * r * r * team_sum<R>(s) / (float)N;
+#pragma unroll
+            for (int k = 0; k < K; ++k)
+#pragma unroll
+                for (int e = 0; e < W; ++e) {
+                    const float d = gv.v[k][e] * r - hv.v[k][e] * c;
+                    gv.v[k][e] = DELTA ? d + res.v[k][e] : d;
+                }
+            store_slice<W, K, R>((char*)dx + off * elem_bytes(dxdt), dxdt, t, units, gv);
+            if constexpr (DELTA) store_slice<W, K, R>((char*)ddelta + off * elem_bytes(dddt), dddt, t, units, gv);
+        }
     }
 
-    // The wave's teams hold the same columns in lanes t, t + R, ...: an xor-butterfly over those lane
-    // groups leaves every lane with the wave's sum.
+    // Unit by unit: the wave's teams hold the same columns in lanes t, t + R, ... (an xor-butterfly over those lane
+    // groups leaves every lane with the wave's sum), then the block's waves are added in wave order.
 #pragma unroll
-    for (int k = 0; k < K; ++k)
+    for (int k = 0; k < K; ++k) {
 #pragma unroll
         for (int e = 0; e < W; ++e) {
             float a = acc.v[k][e];
 #pragma unroll
             for (int m = R; m < 64; m <<= 1) a += __shfl_xor(a, m);
-            if ((threadIdx.x & 63) < R) red[wave][(k * R + t) * W + e] = a;
+            if ((threadIdx.x & 63) < R) red[wave][t * W + e] = a;
         }
-    __syncthreads();
-    // Unit-major columns: element (k R + t) W + e of a wave's slot is column (t + k R) W + e.
-    for (int i = threadIdx.x; i < K * R * W; i += 64 * kBwdWaves) {
-        const int kk = i / (R * W), rem = i - kk * R * W, tt = rem / W, e = rem - tt * W;
-        const int col = (tt + kk * R) * W + e;
-        if (col >= N) continue;
-        float sum = 0.f;
+        __syncthreads();
+        // element t W + e of a wave's slot is column (t + k R) W + e
+        for (int i = threadIdx.x; i < R * W; i += 64 * NWV) {
+            const int col = (i / W + k * R) * W + i % W;
+            if (col < N) {
+                float sum = 0.f;
 #pragma unroll
-        for (int m = 0; m < kBwdWaves; ++m) sum += red[m][i];
-        dw_part[(long long)blockIdx.x * N + col] = sum;
+                for (int m = 0; m < NWV; ++m) sum += red[m][i];
+                dw_part[(long long)blockIdx.x * N + col] = sum;
+            }
+        }
+        __syncthreads();
     }
 }
 
@@ -400,9 +463,15 @@ int with_layout(const Layout& L, bool delta, F&& f) {
 
 long long rows_per_block(const Layout& L) { return 64LL * kWaves / L.R; }
 
+// Waves per backward block: 8, or 4 for rows of more than 48 values per lane, whose resident dw alone is 64
+// values (4 waves leave a wave up to 512 registers; 8 cap it at 256, which such a row exceeds).
+template <int W, int K>
+constexpr int bwd_waves() { return W * K > 48 ? 4 : kBwdWaves; }
+int bwd_waves_of(const Layout& L) { return L.W * L.K > 48 ? 4 : kBwdWaves; }
+
 // Backward grid: enough blocks for one row per team, at most kBwdBlocks.
 long long bwd_blocks(long long M, const Layout& L) {
-    const long long per = 64LL * kBwdWaves / L.R;
+    const long long per = 64LL * bwd_waves_of(L) / L.R;
     const long long b = (M + per - 1) / per;
     return b < kBwdBlocks ? b : kBwdBlocks;
 }
@@ -471,8 +540,9 @@ NNRMS_API int nn_add_rmsnorm_bwd(const void* dy, const void* dh, const void* h, 
         return fail("tensors must be 16-byte aligned");
     const long long P = bwd_blocks(M, L);
     int rc = with_layout(L, dh != nullptr, [&](auto w_, auto k_, auto r_, auto d_) {
-        add_rmsnorm_bwd_kernel<decltype(w_)::value, decltype(k_)::value, decltype(r_)::value, decltype(d_)::value>
-            <<<dim3((unsigned)P), dim3(64 * kBwdWaves), 0, st>>>(dy, dh, h, weight, rstd, dx, ddelta, (float*)workspace,
+        constexpr int NWV = bwd_waves<decltype(w_)::value, decltype(k_)::value>();
+        add_rmsnorm_bwd_kernel<decltype(w_)::value, decltype(k_)::value, decltype(r_)::value, decltype(d_)::value, NWV>
+            <<<dim3((unsigned)P), dim3(64 * NWV), 0, st>>>(dy, dh, h, weight, rstd, dx, ddelta, (float*)workspace,
                                                                (long long)M, (int)N, dy_dtype, h_dtype, dx_dtype,
                                                                dh ? ddelta_dtype : dx_dtype);
         return launched("add_rmsnorm_bwd_kernel");

@@ -172,11 +172,13 @@ def test_rmsnorm_c_abi_rejects_bad_arguments_before_any_launch(kw, msg):
 
 def test_rmsnorm_c_abi_backward_checks_and_workspace():
     L = lib()
-    # one fp32 dw row per block of 8 waves: a block takes 16 rows per pass (32-lane teams) for N <= 1024 with
-    # N % 8 == 0, else 8 (64-lane teams); at most 512 blocks, whose teams then walk further rows
+    # one fp32 dw row per block: a block of 8 waves takes 16 rows per pass (32-lane teams) for N <= 1024 with
+    # N % 8 == 0, else 8 (64-lane teams); above 3072 (more than 48 values per lane) a block has 4 waves and takes 4;
+    # at most 512 blocks, whose teams then walk further rows
     assert L.nn_add_rmsnorm_bwd_workspace_size(8192, 768) == 512 * 768 * 4
     assert L.nn_add_rmsnorm_bwd_workspace_size(7, 768) == 1 * 768 * 4
-    assert L.nn_add_rmsnorm_bwd_workspace_size(7, 4096) == 1 * 4096 * 4
+    assert L.nn_add_rmsnorm_bwd_workspace_size(7, 4096) == 2 * 4096 * 4
+    assert L.nn_add_rmsnorm_bwd_workspace_size(7, 3072) == 1 * 3072 * 4
     assert L.nn_add_rmsnorm_bwd_workspace_size(520, 768) == 33 * 768 * 4
     assert L.nn_add_rmsnorm_bwd_workspace_size(520, 2048) == 65 * 2048 * 4
     assert L.nn_add_rmsnorm_bwd_workspace_size(1 << 20, 33) == 512 * 33 * 4
