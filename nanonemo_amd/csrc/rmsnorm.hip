@@ -352,27 +352,26 @@ __global__ __launch_bounds__(64 * NWV) void add_rmsnorm_bwd_kernel(
     }
 }
 
-// dw[c] = sum over p = 0 .. P-1 of part[p][c], in a fixed order: a block of 16 waves owns 64 columns;
-// wave v adds rows v, v + 16, ..., eight rows per step (eight loads in flight, summed pairwise), and the
-// 16 wave sums are then added in wave order. P = 0 writes zeros.
+// dw[c] = sum over p = 0 .. P-1 of part[p][c], in a fixed order: a block of 16 waves owns 64 columns; wave v
+// loads rows v, v + 16, ..., v + 16 * 31 at once (P <= kBwdBlocks = 512, so one round trip to memory) and adds
+// them as a fixed pairwise tree, and the 16 wave sums are then added in wave order. P = 0 writes zeros.
 __global__ __launch_bounds__(64 * kSumWaves) void colsum_kernel(const float* __restrict__ part,
                                                                 float* __restrict__ dw, int P, int N) {
+    static_assert(kBwdBlocks <= 32 * kSumWaves, "a wave sums at most 32 partial rows");
     __shared__ float red[kSumWaves][64];
     const int v = threadIdx.x >> 6, l = threadIdx.x & 63;
     const int c = blockIdx.x * 64 + l;
-    float acc = 0.f;
-    if (c < N) {
-        constexpr int U = 8, S = U * kSumWaves;
-        for (int p0 = v; p0 < P; p0 += S) {
-            float x[U];
+    float x[32];
 #pragma unroll
-            for (int u = 0; u < U; ++u) {
-                const int p = p0 + u * kSumWaves;
-                x[u] = p < P ? part[(long long)p * N + c] : 0.f;
-            }
-            acc += ((x[0] + x[1]) + (x[2] + x[3])) + ((x[4] + x[5]) + (x[6] + x[7]));
-        }
+    for (int u = 0; u < 32; ++u) {
+        const int p = v + u * kSumWaves;
+        x[u] = c < N && p < P ? part[(long long)p * N + c] : 0.f;
     }
+#pragma unroll
+    for (int w = 16; w > 0; w >>= 1)
+#pragma unroll
+        for (int u = 0; u < w; ++u) x[u] += x[u + w];
+    const float acc = x[0];
     red[v][l] = acc;
     __syncthreads();
     if (v == 0 && c < N) {
