@@ -58,3 +58,48 @@ def test_noalloc_backward_rejects_shapes_beyond_its_array():
     assert L.nn_fa_bwd_workspace_size(B, H, KVH, T, D) > 32 << 20
     rc = L.nn_fa_bwd_noalloc(*([None] * 9), B, H, KVH, T, D, DTYPE_BF16, 0.125, torch.cuda.current_stream().cuda_stream)
     assert rc != 0 and b"scratch" in L.nn_fa_last_error()
+
+
+def test_noalloc_backward_captures_into_a_graph_without_a_workspace():
+    # The caller it exists for: a HIP-graph capture of fwd + bwd whose only buffers are the inputs and outputs
+    # (nothing is allocated for the backward). Replays, with the outputs poisoned and eager work in between, equal
+    # the eager nn_fa_bwd with a caller workspace bit for bit.
+    from nanonemo_amd.kernels.hip import DTYPE_BF16, check, lib
+
+    L = lib()
+    B, H, KVH, T, D = 2, 12, 4, 384, 64
+    print(f"\n[case] graph capture of nn_fa_fwd + nn_fa_bwd_noalloc B={B} H={H} KVH={KVH} T={T} D={D}", flush=True)
+    q, k, v, do = (t.cuda() for t in make_inputs(B, H, KVH, T, D, torch.bfloat16, seed=8))
+    o, lse = torch.empty_like(q), torch.empty(B, H, T, device="cuda")
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    p = lambda t: t.data_ptr()  # noqa: E731
+
+    def launch(st):
+        check(L.nn_fa_fwd(p(q), p(k), p(v), p(o), p(lse), B, H, KVH, T, D, DTYPE_BF16, 0.125, st))
+        check(L.nn_fa_bwd_noalloc(p(do), p(q), p(k), p(v), p(o), p(lse), p(dq), p(dk), p(dv), B, H, KVH, T, D,
+                                  DTYPE_BF16, 0.125, st))
+
+    wsb = L.nn_fa_bwd_workspace_size(B, H, KVH, T, D)
+    ws = torch.empty(wsb, dtype=torch.uint8, device="cuda")
+    ref = [torch.empty_like(t) for t in (dq, dk, dv)]
+    sp = torch.cuda.current_stream().cuda_stream
+    launch(sp)  # first call on the device looks the array up, outside the capture
+    check(L.nn_fa_bwd(p(do), p(q), p(k), p(v), p(o), p(lse), *(p(t) for t in ref), p(ws), wsb, B, H, KVH, T, D,
+                      DTYPE_BF16, 0.125, sp))
+    o_ref, lse_ref = o.clone(), lse.clone()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        launch(torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    for i in range(3):
+        for t in (o, lse, dq, dk, dv):
+            t.fill_(float("nan"))
+        junk = torch.randn(1 << 20, device="cuda") * i
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        for name, a, r in (("o", o, o_ref), ("lse", lse, lse_ref), ("dq", dq, ref[0]), ("dk", dk, ref[1]),
+                           ("dv", dv, ref[2])):
+            assert torch.equal(a, r), f"replay {i}: {name} differs"
+        del junk
