@@ -24,6 +24,9 @@ The JSON line also carries:
                 launch (forward 4*D, dK/dV 6*D, dQ 2*D per causal pair) / its mean launch time, against
                 the dense BF16/FP16 MFMA peak of 2.5 PFLOP/s; traffic = its HBM bytes per launch from the
                 committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary of this workload;
+  clock         the GFX clock (median of the SMU's per-XCD readings through amdsmi) and socket power while
+                the dK/dV kernel alone, then the whole step, run back to back; roofline.frac_at_sclk is the
+                dominant kernel's fraction of the peak scaled to that clock (the published peak assumes 2.4 GHz);
   cpu_baseline  the reference's plain-PyTorch attention on BASELINE config 1 (fp32, B=1, T=256), forward +
                 autograd backward, both of its forms (SDPA math and explicit matmuls), on the host CPUs;
   kernels       per-kernel mean times (nn_fa_bwd = the dQ kernel, which also runs the preprocessing pass,
@@ -97,6 +100,77 @@ def _norm_launches(L, M, dev, sp):
         "bwd_bytes": M * N * (2 + 4 + 4 + 4 + 2) + 4 * M,
         "keep": keep,
     }
+
+
+def gfx_clock(dev, enqueue, seconds=0.3):
+    """The GFX (shader) clock the device runs at under a given load: enqueue() (device work, issued back to back
+    in batches) repeats for about `seconds` while a thread samples the SMU's per-XCD current GFX clock and the
+    socket power through amdsmi every few ms. Returns the median (and p10 / p90) over the samples of the mean
+    over the XCDs, the median power, and the clock ceiling; {"error": ...} where amdsmi is unavailable."""
+    import threading
+
+    import torch
+
+    try:
+        import amdsmi
+
+        amdsmi.amdsmi_init()
+    except Exception as exc:  # noqa: BLE001 -- the measurement is optional
+        return {"error": f"amdsmi unavailable: {exc}"}
+    try:
+        handles = amdsmi.amdsmi_get_processor_handles()
+        handle = handles[0] if len(handles) == 1 else None
+        if handle is None:  # several GPUs visible: the one whose PCI address is cuda's device
+            props = torch.cuda.get_device_properties(dev)
+            want = f"{getattr(props, 'pci_domain_id', 0):04x}:{getattr(props, 'pci_bus_id', -1):02x}:"
+            handle = next((h for h in handles if amdsmi.amdsmi_get_gpu_device_bdf(h).lower().startswith(want)), None)
+        if handle is None:
+            return {"error": "no amdsmi handle matches the device"}
+        ceiling = amdsmi.amdsmi_get_clock_info(handle, amdsmi.AmdSmiClkType.GFX).get("max_clk")
+        samples, stop = [], threading.Event()
+
+        def sampler():
+            while not stop.is_set():
+                m = amdsmi.amdsmi_get_gpu_metrics_info(handle)
+                clks = [c for c in (m.get("current_gfxclks") or []) if isinstance(c, int)]
+                pw = m.get("current_socket_power")
+                if clks:
+                    samples.append((time.perf_counter(), sum(clks) / len(clks), pw if isinstance(pw, int) else None,
+                                    m.get("system_clock_counter")))
+                time.sleep(0.003)
+
+        th = threading.Thread(target=sampler, daemon=True)
+        torch.cuda.synchronize()
+        th.start()
+        t0 = time.perf_counter()
+        while time.perf_counter() - t0 < seconds:
+            enqueue()
+            torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        stop.set()
+        th.join()
+        window = [x for x in samples if t0 + 0.03 < x[0] < t1]  # past the first 30 ms of ramp
+        inside = sorted(x[1] for x in window)
+        power = [x[2] for x in window if x[2] is not None]
+        if not inside:
+            return {"error": "no clock samples"}
+        return {
+            "gfx_mhz_median": round(statistics.median(inside)),
+            "gfx_mhz_p10": round(inside[len(inside) // 10]),
+            "gfx_mhz_p90": round(inside[(9 * len(inside)) // 10]),
+            "samples": len(inside),
+            # distinct SMU metric tables among the samples (its timestamp), i.e. how many readings are independent
+            "smu_updates": len({x[3] for x in window}),
+            "socket_power_w_median": statistics.median(power) if power else None,
+            "gfx_mhz_max": ceiling,
+        }
+    except Exception as exc:  # noqa: BLE001
+        return {"error": f"amdsmi query failed: {exc}"}
+    finally:
+        try:
+            amdsmi.amdsmi_shut_down()
+        except Exception:  # noqa: BLE001
+            pass
 
 
 def parse():
@@ -466,6 +540,12 @@ def main():
         e1.record(stream)
         e1.synchronize()
         kern_us[name] = e0.elapsed_time(e1) * 1e3 / reps
+    # The clock the chip holds under this load (the 2.5 PFLOP/s peak assumes 2.4 GHz): sampled while the dK/dV
+    # kernel alone, then the whole C-ABI step, run back to back.
+    clocks = {
+        "bwd_dkdv": gfx_clock(dev, lambda: [check(launches["bwd_dkdv"]()) for _ in range(100)]),
+        "step": gfx_clock(dev, lambda: [step_abi() for _ in range(50)]),
+    }
 
     # ---- layout fusion: the same fwd+bwd starting from the projection layout (B, T, heads, hd) ----
     # (after the per-kernel timings: its new allocations slow the next ~300 steps, see the warmup note)
@@ -621,6 +701,7 @@ def main():
 
     value = f_all / (ms * 1e-3) / 1e12
     props = torch.cuda.get_device_properties(dev)
+    sclk = (clocks["bwd_dkdv"] if dominant == "bwd_dkdv" else clocks["step"]).get("gfx_mhz_median")
     out = {
         "metric": METRIC,
         "value": round(value, 2),
@@ -700,7 +781,12 @@ def main():
             "unit": "TFLOP/s",
             "frac": round(kern_tflops[dominant] / PEAK_TFLOPS, 4),
             "traffic": traffic,
+            # the same peak scaled to the GFX clock measured while the kernel ran back to back
+            "sclk_mhz": sclk,
+            "peak_at_sclk": round(PEAK_TFLOPS * sclk / 2400.0, 1) if sclk else None,
+            "frac_at_sclk": round(kern_tflops[dominant] / (PEAK_TFLOPS * sclk / 2400.0), 4) if sclk else None,
         },
+        "clock": clocks,
         "kernels": {
             "fwd_us": round(kern_us["fwd"], 2),
             "fwd_tflops": round(kern_tflops["fwd"], 2),
