@@ -2,6 +2,7 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--dtype bf16|fp16] [--batch 8] [--seq 1024]
     python bench.py --sweep        # step and per-kernel times over the SWEEP shapes, one JSON line each
+    python bench.py --probes       # VALU/MFMA co-issue table and shader clock under load (probe library)
 
 A step is one forward + backward of the hot path through the drop-in torch.library ops (nanonemo::flash_attn
 then nanonemo::flash_attn_bwd, which call the C ABI of include/nanonemo_fa.h) on synthetic N(0,1) inputs
@@ -102,11 +103,13 @@ def _norm_launches(L, M, dev, sp):
     }
 
 
-def gfx_clock(dev, enqueue, seconds=0.3):
+def gfx_clock(dev, enqueue, seconds=2.5):
     """The GFX (shader) clock the device runs at under a given load: enqueue() (device work, issued back to back
     in batches) repeats for about `seconds` while a thread samples the SMU's per-XCD current GFX clock and the
-    socket power through amdsmi every few ms. Returns the median (and p10 / p90) over the samples of the mean
-    over the XCDs, the median power, and the clock ceiling; {"error": ...} where amdsmi is unavailable."""
+    socket power through amdsmi every few ms. The SMU refreshes those readings about once a second, so only the
+    tables published after the load started count. Returns the median (and p10 / p90) over the samples of the
+    mean over the XCDs, the median power, the number of distinct tables and the clock ceiling; {"error": ...}
+    where amdsmi is unavailable or no table was published in the window."""
     import threading
 
     import torch
@@ -141,6 +144,9 @@ def gfx_clock(dev, enqueue, seconds=0.3):
 
         th = threading.Thread(target=sampler, daemon=True)
         torch.cuda.synchronize()
+        # The SMU refreshes its table about once a second: the table current now describes the time before the
+        # load, so its samples are dropped.
+        before = amdsmi.amdsmi_get_gpu_metrics_info(handle).get("system_clock_counter")
         th.start()
         t0 = time.perf_counter()
         while time.perf_counter() - t0 < seconds:
@@ -149,18 +155,19 @@ def gfx_clock(dev, enqueue, seconds=0.3):
         t1 = time.perf_counter()
         stop.set()
         th.join()
-        window = [x for x in samples if t0 + 0.03 < x[0] < t1]  # past the first 30 ms of ramp
+        window = [x for x in samples if t0 < x[0] < t1 and x[3] != before]
         inside = sorted(x[1] for x in window)
         power = [x[2] for x in window if x[2] is not None]
         if not inside:
-            return {"error": "no clock samples"}
+            return {"error": f"the SMU metrics table did not refresh during the {seconds} s window"}
+        updates = len({x[3] for x in window})
         return {
             "gfx_mhz_median": round(statistics.median(inside)),
             "gfx_mhz_p10": round(inside[len(inside) // 10]),
             "gfx_mhz_p90": round(inside[(9 * len(inside)) // 10]),
             "samples": len(inside),
             # distinct SMU metric tables among the samples (its timestamp), i.e. how many readings are independent
-            "smu_updates": len({x[3] for x in window}),
+            "smu_updates": updates,
             "socket_power_w_median": statistics.median(power) if power else None,
             "gfx_mhz_max": ceiling,
         }
@@ -191,6 +198,9 @@ def parse():
     p.add_argument("--prewarm", type=float, default=1.0, help="seconds of untimed steps after the warmup")
     p.add_argument("--sweep", action="store_true",
                    help="instead of the headline line: one JSON line per shape of SWEEP (step and per-kernel times)")
+    p.add_argument("--probes", action="store_true",
+                   help="instead of the headline line: the VALU/MFMA co-issue table and the shader clock under load "
+                   "(nanonemo_amd/csrc/probe.hip), one JSON line")
     return p.parse_args()
 
 
@@ -375,10 +385,79 @@ def cpu_baseline(budget_s):
     }
 
 
+def probes():
+    """The measurements the kernels' design rests on, from the probe library (nanonemo_amd/csrc/probe.hip):
+    - coissue: time per 32x32x16 bf16 MFMA per SIMD when every MFMA is followed by K independent fp32 FMAs, with
+      1-4 waves resident per SIMD (as cycles at 2.4 GHz, converted from the measured rate);
+    - clock: the shader clock from per-wave s_memtime / s_memrealtime stamps around back-to-back MFMAs (1 and 4
+      waves per SIMD) and FMAs only (4 waves per SIMD), and the shader cycles per MFMA with one wave per SIMD."""
+    import torch
+
+    from nanonemo_amd.build import PROBE_LIB
+
+    if not PROBE_LIB.exists():
+        raise RuntimeError(f"{PROBE_LIB} is not built; run `python -m nanonemo_amd.build`")
+    P = ctypes.CDLL(str(PROBE_LIB))
+    P.nn_probe_coissue.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
+    P.nn_probe_clock.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p,
+                                 ctypes.c_void_p]
+    P.nn_probe_last_error.restype = ctypes.c_char_p
+
+    def ok(rc):
+        if rc != 0:
+            raise RuntimeError(P.nn_probe_last_error().decode())
+
+    dev = torch.device("cuda:0")
+    ncu = torch.cuda.get_device_properties(dev).multi_processor_count
+    sp = torch.cuda.current_stream().cuda_stream
+    n = 4000
+    sink = torch.empty(4 * ncu * 256, device=dev)
+    coissue = {}
+    for wps in (1, 2, 3, 4):
+        blocks = ncu * wps  # 4 waves per block: one per SIMD of its CU
+        row = {}
+        for k in (0, 4, 8, 12, 16):
+            for _ in range(2):
+                ok(P.nn_probe_coissue(k, blocks, n, sink.data_ptr(), sp))
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            ok(P.nn_probe_coissue(k, blocks, n, sink.data_ptr(), sp))
+            e1.record()
+            e1.synchronize()
+            s = e0.elapsed_time(e1) * 1e-3
+            mfma_per_simd = wps * 4 * n
+            row[f"K={k}"] = round(s / mfma_per_simd * 2.4e9, 1)
+        coissue[f"{wps} waves/SIMD"] = row
+    clock = {}
+    for label, mode, wps in (("mfma, 1 wave/SIMD", 0, 1), ("mfma, 4 waves/SIMD", 0, 4), ("fma, 4 waves/SIMD", 1, 4)):
+        blocks = ncu * wps
+        stamps = torch.zeros(blocks * 16, dtype=torch.int64, device=dev)
+        for _ in range(3):
+            ok(P.nn_probe_clock(mode, blocks, 20000, stamps.data_ptr(), sink.data_ptr(), sp))
+        torch.cuda.synchronize()
+        st = stamps.view(-1, 4).cpu().double()
+        mhz = ((st[:, 1] - st[:, 0]) / ((st[:, 3] - st[:, 2]) / 100.0)).sort().values
+        entry = {"mhz_median": round(mhz[len(mhz) // 2].item()), "mhz_min": round(mhz[0].item()),
+                 "mhz_max": round(mhz[-1].item())}
+        if mode == 0 and wps == 1:  # (with several waves a wave's lifetime is not the SIMD's busy time)
+            entry["shader_cycles_per_mfma_per_wave"] = round(((st[:, 1] - st[:, 0]).median() / (4 * 20000)).item(), 1)
+        clock[label] = entry
+    print(json.dumps({"probes": {
+        "coissue_cycles_per_mfma_per_simd_at_2400mhz": coissue,
+        "coissue_how": "each wave: 32x32x16 bf16 MFMAs on 4 accumulators, each followed by K independent fp32 FMAs; "
+                       "time per MFMA per SIMD from HIP events, as cycles at 2.4 GHz (a lone MFMA is 32 shader cycles)",
+        "clock": clock,
+        "cus": ncu,
+    }}), flush=True)
+
+
 def main():
     args = parse()
     if args.sweep and args.gpus == 1:
         sweep(args)
+        return
+    if args.probes and args.gpus == 1:
+        probes()
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(

@@ -23,6 +23,10 @@ ROOT = PKG.parent
 SRCS = [PKG / "csrc" / "flash_attn.hip", PKG / "csrc" / "rope.hip", PKG / "csrc" / "rmsnorm.hip"]
 LIB_DIR = PKG / "lib"
 LIB = LIB_DIR / "libnanonemo_fa.so"
+# Measurement probes for `bench.py --probes` (VALU/MFMA co-issue, shader clock), a library of their own so that
+# the attention library's ABI stays what include/*.h declares.
+PROBE_SRCS = [PKG / "csrc" / "probe.hip"]
+PROBE_LIB = LIB_DIR / "libnanonemo_probe.so"
 ARCH = "gfx950"
 
 # -packed-fp32-ops: keep v_pk_{add,mul,fma}_f32 out of the generated code (those packed forms have
@@ -58,11 +62,10 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found (looked at $HIPCC, /opt/rocm/bin/hipcc and PATH)")
 
 
-def build(verbose: bool = False) -> Path:
-    """Compile the HIP library (always recompiles) and return its path."""
+def _compile(srcs: list[Path], lib: Path, verbose: bool) -> Path:
     LIB_DIR.mkdir(parents=True, exist_ok=True)
-    tmp = LIB.with_suffix(".so.tmp")
-    cmd = [hipcc(), *HIPCC_FLAGS, f"-I{ROOT / 'include'}", "-o", str(tmp), *(str(s) for s in SRCS)]
+    tmp = lib.with_suffix(".so.tmp")
+    cmd = [hipcc(), *HIPCC_FLAGS, f"-I{ROOT / 'include'}", "-o", str(tmp), *(str(s) for s in srcs)]
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
@@ -72,8 +75,14 @@ def build(verbose: bool = False) -> Path:
         raise RuntimeError(f"hipcc failed ({res.returncode}):\n{log}")
     if verbose and log.strip():
         print(log, flush=True)
-    os.replace(tmp, LIB)  # atomic: a process that already mapped the old file keeps it
-    return LIB
+    os.replace(tmp, lib)  # atomic: a process that already mapped the old file keeps it
+    return lib
+
+
+def build(verbose: bool = False) -> Path:
+    """Compile the HIP library and the measurement probes (always recompiles); return the library's path."""
+    _compile(PROBE_SRCS, PROBE_LIB, verbose)
+    return _compile(SRCS, LIB, verbose)
 
 
 if __name__ == "__main__":

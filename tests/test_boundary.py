@@ -42,6 +42,24 @@ def test_abi_version():
     assert lib().nn_fa_abi_version() == ABI_VERSION
 
 
+def test_probe_library_is_separate_and_rejects_bad_arguments():
+    # bench.py --probes' measurement kernels live in their own library: the attention library exports none of
+    # them, and the probe entry points refuse arguments outside what their kernels assume (no launch then).
+    from nanonemo_amd.build import PROBE_LIB
+
+    assert PROBE_LIB.exists(), "run `python -m nanonemo_amd.build` first"
+    P = ctypes.CDLL(str(PROBE_LIB))
+    for name in ("nn_probe_coissue", "nn_probe_clock", "nn_probe_last_error"):
+        assert hasattr(P, name) and not hasattr(lib(), name), name
+    P.nn_probe_coissue.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
+    P.nn_probe_clock.argtypes = [ctypes.c_int] * 3 + [ctypes.c_void_p] * 3
+    P.nn_probe_last_error.restype = ctypes.c_char_p
+    assert P.nn_probe_coissue(8, 0, 10, 16, None) != 0 and b"invalid" in P.nn_probe_last_error()
+    assert P.nn_probe_coissue(5, 1, 10, 16, None) != 0 and b"k must be" in P.nn_probe_last_error()
+    assert P.nn_probe_clock(2, 1, 10, 16, 16, None) != 0 and b"mode must be" in P.nn_probe_last_error()
+    assert P.nn_probe_clock(0, 1, 10, None, 16, None) != 0 and b"invalid" in P.nn_probe_last_error()
+
+
 def _dkdv_split(B, H, KVH, T):
     """Blocks sharing one dK/dV unit pair: 1 when the B*KVH*ceil(nkb/2) pairs fill 256 CUs, else up to 16,
     keeping at least 8 of a pair's (H/KVH)*(nkb+1) iterations per split, and none where 16 times a unit's
