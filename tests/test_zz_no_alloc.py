@@ -13,23 +13,24 @@ from tests.common import make_inputs
 pytestmark = pytest.mark.gpu
 
 
-def _run_both(L, B, H, KVH, T, D, seed):
-    from nanonemo_amd.kernels.hip import DTYPE_BF16, check
+def _run_both(L, B, H, KVH, T, D, seed, dtype=torch.bfloat16):
+    from nanonemo_amd.kernels.hip import DTYPE_BF16, DTYPE_F16, check
 
-    print(f"\n[case] nn_fa_bwd_noalloc vs nn_fa_bwd B={B} H={H} KVH={KVH} T={T} D={D} seed={seed}", flush=True)
-    q, k, v, do = (t.cuda() for t in make_inputs(B, H, KVH, T, D, torch.bfloat16, seed=seed))
+    code = DTYPE_BF16 if dtype == torch.bfloat16 else DTYPE_F16
+    print(f"\n[case] nn_fa_bwd_noalloc vs nn_fa_bwd B={B} H={H} KVH={KVH} T={T} D={D} {dtype} seed={seed}", flush=True)
+    q, k, v, do = (t.cuda() for t in make_inputs(B, H, KVH, T, D, dtype, seed=seed))
     o, lse = torch.empty_like(q), torch.empty(B, H, T, device="cuda")
     sp = torch.cuda.current_stream().cuda_stream
     p = lambda t: t.data_ptr()  # noqa: E731
-    check(L.nn_fa_fwd(p(q), p(k), p(v), p(o), p(lse), B, H, KVH, T, D, DTYPE_BF16, D ** -0.5, sp))
+    check(L.nn_fa_fwd(p(q), p(k), p(v), p(o), p(lse), B, H, KVH, T, D, code, D ** -0.5, sp))
     wsb = L.nn_fa_bwd_workspace_size(B, H, KVH, T, D)
     ws = torch.empty(wsb, dtype=torch.uint8, device="cuda")
     ref = [torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)]
     check(L.nn_fa_bwd(p(do), p(q), p(k), p(v), p(o), p(lse), *(p(t) for t in ref), p(ws), wsb, B, H, KVH, T, D,
-                      DTYPE_BF16, D ** -0.5, sp))
+                      code, D ** -0.5, sp))
     got = [torch.full_like(t, float("nan")) for t in ref]
     check(L.nn_fa_bwd_noalloc(p(do), p(q), p(k), p(v), p(o), p(lse), *(p(t) for t in got), B, H, KVH, T, D,
-                              DTYPE_BF16, D ** -0.5, sp))
+                              code, D ** -0.5, sp))
     torch.cuda.synchronize()
     for name, a, r in zip(("dq", "dk", "dv"), got, ref):
         assert torch.equal(a, r), f"{name} differs at B={B} H={H} KVH={KVH} T={T}: max |diff| {(a.float() - r.float()).abs().max().item()}"
@@ -48,6 +49,14 @@ def test_noalloc_backward_matches_workspace_backward_twice(first, second):
     L = lib()
     _run_both(L, *first, seed=5)
     _run_both(L, *second, seed=6)
+
+
+def test_noalloc_backward_matches_workspace_backward_in_fp16():
+    from nanonemo_amd.kernels.hip import lib
+
+    L = lib()
+    _run_both(L, 2, 12, 1, 1024, 64, seed=9, dtype=torch.float16)  # split dK/dV
+    _run_both(L, 3, 8, 4, 129, 64, seed=10, dtype=torch.float16)
 
 
 def test_noalloc_backward_rejects_shapes_beyond_its_array():
