@@ -28,6 +28,9 @@ The JSON line also carries:
   clock         the GFX clock (median of the SMU's per-XCD readings through amdsmi) and socket power while
                 the dK/dV kernel alone, then the whole step, run back to back; roofline.frac_at_sclk is the
                 dominant kernel's fraction of the peak scaled to that clock (the published peak assumes 2.4 GHz);
+  same_node     PyTorch's own attention on the same GPU (SDPA flash with native GQA, and the reference
+                benchmark's providers: SDPA mem-efficient and math on repeat_interleave'd K/V) beside this
+                build's op, each as fwd + autograd.grad back to back;
   cpu_baseline  the reference's plain-PyTorch attention on BASELINE config 1 (fp32, B=1, T=256), forward +
                 autograd backward, both of its forms (SDPA math and explicit matmuls), on the host CPUs;
   kernels       per-kernel mean times (nn_fa_bwd = the dQ kernel, which also runs the preprocessing pass,
@@ -178,6 +181,65 @@ def gfx_clock(dev, enqueue, seconds=2.5):
             amdsmi.amdsmi_shut_down()
         except Exception:  # noqa: BLE001
             pass
+
+
+def same_node(q, k, v, do, fa, reps):
+    """PyTorch's own attention on the same GPU, as the reference benchmark's providers run it
+    (/root/reference/benchmarks/kernels/flash_attn.py:27-49: SDPA mem-efficient and SDPA math on
+    repeat_interleave'd K/V), plus SDPA's flash backend with native GQA (enable_gqa) where this PyTorch has one,
+    and this build's op through autograd the same way: fwd + autograd.grad w.r.t. q, k, v, back to back on warm
+    caches, mean time per call from HIP events (host_ms: the host's time per call, which exceeds ms where the
+    host, not the GPU, sets the pace)."""
+    import warnings
+
+    import torch
+    import torch.nn.functional as F
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+
+    B, H, T = q.shape[0], q.shape[1], q.shape[2]
+    group = H // k.shape[1]
+    qs, ks, vs = (t.detach().clone().requires_grad_() for t in (q, k, v))
+
+    def sdpa(backend, gqa):
+        def step():
+            with sdpa_kernel([backend]):
+                if gqa:
+                    o = F.scaled_dot_product_attention(qs, ks, vs, is_causal=True, enable_gqa=True)
+                else:
+                    kk, vv = ks.repeat_interleave(group, dim=1), vs.repeat_interleave(group, dim=1)
+                    o = F.scaled_dot_product_attention(qs, kk, vv, is_causal=True)
+            return torch.autograd.grad(o, (qs, ks, vs), do)
+
+        return step
+
+    def ours():
+        return torch.autograd.grad(fa.flash_attn(qs, ks, vs), (qs, ks, vs), do)
+
+    providers = {"this_build_autograd": ours, "sdpa_flash_gqa": sdpa(SDPBackend.FLASH_ATTENTION, True),
+                 "sdpa_mem_efficient": sdpa(SDPBackend.EFFICIENT_ATTENTION, False)}
+    if B * H * T * T <= 1 << 27:  # math materialises the B*H*T*T scores
+        providers["sdpa_math"] = sdpa(SDPBackend.MATH, False)
+    out = {}
+    with warnings.catch_warnings():
+        warnings.simplefilter("ignore")
+        for name, fn in providers.items():
+            try:
+                for _ in range(3):
+                    fn()
+                torch.cuda.synchronize()
+                n = reps if name != "sdpa_math" else max(3, reps // 10)
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                t0 = time.perf_counter()
+                e0.record()
+                for _ in range(n):
+                    fn()
+                t1 = time.perf_counter()
+                e1.record()
+                e1.synchronize()
+                out[name] = {"ms": round(e0.elapsed_time(e1) / n, 5), "host_ms": round((t1 - t0) * 1e3 / n, 5)}
+            except Exception as exc:  # noqa: BLE001 -- a backend this PyTorch lacks
+                out[name] = {"error": str(exc).splitlines()[0][:200]}
+    return out
 
 
 def parse():
@@ -753,6 +815,9 @@ def main():
         b_.record(stream)
     torch.cuda.synchronize()
     ref_ms = sorted(a.elapsed_time(b_) for a, b_ in ev)
+    # PyTorch's own attention on this GPU, beside this build's (last: SDPA math's scores are a large new
+    # allocation, which would slow the measurements after it)
+    sdpa_cmp = same_node(q, k, v, do, fa, max(20, args.steps // 2))
 
     e = 2  # bytes per 16-bit element
     pre_alg_bytes = 2 * B * H * T * D * e + 4 * B * H * T
@@ -845,6 +910,12 @@ def main():
             # the RoPE kernel's read of q (its q_rot write moves into the forward) and rope_qk_bwd's read and
             # write of dq
             "q_trip_bytes_removed": 3 * qbytes,
+        },
+        "same_node": {
+            "how": "fwd + autograd.grad back to back, warm caches, HIP events; SDPA as the reference benchmark runs it "
+            "(repeat_interleave'd K/V), flash with native GQA; op_pair = this build's two ops without autograd",
+            "this_build_op_pair_ms": round(op_ms, 5),
+            **sdpa_cmp,
         },
         "layout_fusion": {
             "from": "projection layout (B, T, heads, hd)",

@@ -127,11 +127,18 @@ def _setup_context(ctx, inputs, output):
     q, k, v = inputs
     o, lse = output
     ctx.save_for_backward(q, k, v, o, lse)
+    # lse's gradient is ignored, so autograd need not fill a zero tensor for it on every backward.
+    ctx.set_materialize_grads(False)
+
+
+def _d_out(d_o, o):
+    """The gradient reaching o; zeros when o itself was not used (only lse was), as a materialised grad would be."""
+    return torch.zeros_like(o) if d_o is None else d_o
 
 
 def _backward(ctx, d_o, _d_lse):
     q, k, v, o, lse = ctx.saved_tensors
-    return _flash_attn_bwd(d_o, q, k, v, o, lse)
+    return _flash_attn_bwd(_d_out(d_o, o), q, k, v, o, lse)
 
 
 _flash_attn.register_autograd(_backward, setup_context=_setup_context)
@@ -224,7 +231,7 @@ def _(d_o, q, k, v, o, lse):
 
 def _backward_bthd(ctx, d_o, _d_lse):
     q, k, v, o, lse = ctx.saved_tensors
-    return _flash_attn_bthd_bwd(d_o, q, k, v, o, lse)
+    return _flash_attn_bthd_bwd(_d_out(d_o, o), q, k, v, o, lse)
 
 
 _flash_attn_bthd.register_autograd(_backward_bthd, setup_context=_setup_context)
@@ -326,11 +333,12 @@ def _setup_context_rope(ctx, inputs, output):
     _, k, v, cos, sin = inputs
     o, lse, q_rot = output
     ctx.save_for_backward(q_rot, k, v, o, lse, cos, sin)
+    ctx.set_materialize_grads(False)  # the gradients of lse and q_rot are ignored
 
 
 def _backward_rope(ctx, d_o, _d_lse, _d_q_rot):
     q_rot, k, v, o, lse, cos, sin = ctx.saved_tensors
-    dq, dk, dv = _flash_attn_bthd_rope_bwd(d_o, q_rot, k, v, o, lse, cos, sin)
+    dq, dk, dv = _flash_attn_bthd_rope_bwd(_d_out(d_o, o), q_rot, k, v, o, lse, cos, sin)
     return dq, dk, dv, None, None
 
 

@@ -107,15 +107,20 @@ def _(dy, dh, h, weight, rstd, dx_dtype, ddelta_dtype):
 
 def _setup_context(ctx, inputs, output):
     x, delta, weight, eps, out_dtype = inputs
-    _, h, rstd = output
+    y, h, rstd = output
     ctx.save_for_backward(h if delta is not None else x, weight, rstd)
     ctx.x_dtype = x.dtype
+    ctx.y_dtype = y.dtype
     ctx.delta_dtype = delta.dtype if delta is not None else None
+    # rstd's gradient is ignored, so autograd need not fill a zero tensor for it on every backward.
+    ctx.set_materialize_grads(False)
 
 
 def _backward(ctx, dy, dh, _drstd):
     h, weight, rstd = ctx.saved_tensors
     has_delta = ctx.delta_dtype is not None
+    if dy is None:  # y unused downstream
+        dy = torch.zeros(h.shape, dtype=ctx.y_dtype, device=h.device)
     if has_delta and dh is None:  # h unused downstream
         dh = torch.zeros_like(h)
     dx, dd, dw = _bwd(dy, dh if has_delta else None, h, weight, rstd, ctx.x_dtype, ctx.delta_dtype)

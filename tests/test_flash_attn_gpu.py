@@ -310,6 +310,25 @@ def test_deterministic_backward():
         assert all(torch.equal(a, b) for a, b in zip(g1, g2)), shape
 
 
+def test_backward_when_only_lse_is_used():
+    # lse's gradient is ignored (as in the reference), and autograd passes no gradient for an unused o: the
+    # backward then runs on a zero dO, so every input gradient is exactly zero.
+    fa = _fa()
+    q, k, v, _ = (t.to(DEV).requires_grad_() for t in make_inputs(2, 12, 4, 200, 64, torch.bfloat16, seed=4))
+    _, lse = fa._flash_attn(q, k, v)
+    lse.sum().backward()
+    for t in (q, k, v):
+        assert t.grad is not None and torch.equal(t.grad, torch.zeros_like(t))
+    # and with o used, autograd's result is the backward op's on the same dO, bit for bit
+    q2, k2, v2 = (t.detach().clone().requires_grad_() for t in (q, k, v))
+    do = torch.randn_like(q)
+    o = fa.flash_attn(q2, k2, v2)
+    o.backward(do)
+    o_, lse_ = fa._flash_attn(q.detach(), k.detach(), v.detach())
+    for a, b in zip((q2.grad, k2.grad, v2.grad), fa._flash_attn_bwd(do, q.detach(), k.detach(), v.detach(), o_, lse_)):
+        assert torch.equal(a, b)
+
+
 def test_opcheck():
     fa = _fa()
     for dtype in (torch.float16, torch.bfloat16):

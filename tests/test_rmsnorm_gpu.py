@@ -98,6 +98,29 @@ def test_backward_is_deterministic():
         assert torch.equal(a, b)
 
 
+def test_gradient_through_one_output_only():
+    # Autograd passes no gradient for an unused output (the op does not ask it to fill zeros): only the
+    # residual used gives dx = ddelta = 1 and dw = 0; only the normalised output used gives the same
+    # gradients as an explicit zero gradient for the residual.
+    x, d, w = _inputs(520, 768, torch.float32, torch.bfloat16)
+    y, h = _mod().add_rms_norm(x, d, w, EPS)
+    h.sum().backward()
+    assert torch.equal(x.grad, torch.ones_like(x)) and torch.equal(d.grad, torch.ones_like(d))
+    assert torch.equal(w.grad, torch.zeros_like(w))
+    gy = torch.randn(520, 768, device="cuda")
+    grads = []
+    for with_zero_dh in (False, True):
+        xs, ds, ws = (t.detach().clone().requires_grad_() for t in (x, d, w))
+        y, h = _mod().add_rms_norm(xs, ds, ws, EPS)
+        loss = (y.float() * gy).sum()
+        if with_zero_dh:
+            loss = loss + (h * 0).sum()
+        loss.backward()
+        grads.append((xs.grad, ds.grad, ws.grad))
+    for a, b in zip(*grads):
+        assert torch.equal(a, b)
+
+
 def test_empty_rows():
     x = torch.empty(0, 768, device="cuda", requires_grad=True)
     d = torch.empty(0, 768, device="cuda", requires_grad=True)
