@@ -719,31 +719,55 @@ def main():
     views_ms = timed(step_views, args.steps)
     fused_ms = timed(step_fused, args.steps)
 
-    # ---- q's RoPE folded into the attention: rope_qk + the layout-fused pair + rope_qk_bwd, against k's RoPE
-    # alone + the rope-fused pair + k's RoPE backward (the q tensor's trip through the RoPE kernels removed) ----
-    from nanonemo_amd.kernels.hip import rope as rp
+    # ---- q's RoPE folded into the attention, against the separate RoPE kernel, as GPU time: the C-ABI flows
+    # back to back, timed with HIP events on the launch stream (the ops' host cost would set the pace of a loop of
+    # op calls). Separate: nn_rope_qk(q, k) + the strided pair + nn_rope_qk_bwd(dq, dk). Fused: nn_rope_qk on k
+    # alone + nn_fa_fwd_rope_strided / nn_fa_bwd_rope_strided (q rotated in the forward's registers, dq rotated
+    # back in the dQ kernel) + nn_rope_qk_bwd on dk alone. ----
+    from nanonemo_amd.kernels.hip import check_rope as _chk_rope
+    from nanonemo_amd.kernels.hip import strides3 as _s3
     from nanonemo_amd.model import rope_tables as _tables
 
     cos_f, sin_f = (t.to(dev) for t in _tables(D, T, 10000.0))
-    q_empty = qp.new_empty(B, T, 0, D)
+    rq, rk, rdq, rdk, rdq2, rdk2 = (torch.empty_like(t) for t in (qp, kp, qp, kp, qp, kp))
+    ro, rlse, rqrot = torch.empty_like(qp), torch.empty(B, H, T, device=dev), torch.empty_like(qp)
+    rdv = torch.empty_like(vp)
+    s_att_q, s_att_kv = _s3(T * H * D, D, H * D), _s3(T * KVH * D, D, KVH * D)   # (batch, head, row) strides
+    s_rope_q, s_rope_kv = _s3(T * H * D, H * D, D), _s3(T * KVH * D, KVH * D, D)  # (batch, row, head) strides
+    P = lambda t: t.data_ptr()  # noqa: E731
 
-    def step_rope_separate():
-        qr, kr = rp._rope_qk(qp, kp, cos_f, sin_f)
-        o2, lse2 = fa._flash_attn_bthd(qr, kr, vp)
-        dqr, dkr, dvr = fa._flash_attn_bthd_bwd(dop, qr, kr, vp, o2, lse2)
-        return rp._rope_qk_bwd(dqr, dkr, cos_f, sin_f), dvr
+    def rope_flow(fused):
+        hq = 0 if fused else H  # the fused flow rotates k alone
+        _chk_rope(L.nn_rope_qk(P(qp), P(rq), P(kp), P(rk), P(cos_f), P(sin_f), B, T, hq, KVH, D, s_rope_q, s_rope_kv,
+                               T, dt_code, sp))
+        if fused:
+            check(L.nn_fa_fwd_rope_strided(P(qp), P(rk), P(vp), P(ro), P(rlse), P(rqrot), P(cos_f), P(sin_f), T, B, H,
+                                           KVH, T, D, s_att_q, s_att_kv, dt_code, scale, sp))
+            check(L.nn_fa_bwd_rope_strided(P(dop), P(rqrot), P(rk), P(vp), P(ro), P(rlse), P(rdq), P(rdk), P(rdv),
+                                           P(ws), ws_bytes, P(cos_f), P(sin_f), T, B, H, KVH, T, D, s_att_q,
+                                           s_att_kv, dt_code, scale, sp))
+        else:
+            check(L.nn_fa_fwd_strided(P(rq), P(rk), P(vp), P(ro), P(rlse), B, H, KVH, T, D, s_att_q, s_att_kv, dt_code,
+                                      scale, sp))
+            check(L.nn_fa_bwd_strided(P(dop), P(rq), P(rk), P(vp), P(ro), P(rlse), P(rdq), P(rdk), P(rdv), P(ws),
+                                      ws_bytes, B, H, KVH, T, D, s_att_q, s_att_kv, dt_code, scale, sp))
+        _chk_rope(L.nn_rope_qk_bwd(P(rdq), P(rdq2), P(rdk), P(rdk2), P(cos_f), P(sin_f), B, T, hq, KVH, D, s_rope_q,
+                                   s_rope_kv, T, dt_code, sp))
 
-    def step_rope_fused():
-        kr = rp._rope_qk(q_empty, kp, cos_f, sin_f)[1]
-        o2, lse2, qr = fa._flash_attn_bthd_rope(qp, kr, vp, cos_f, sin_f)
-        dq2, dkr, dvr = fa._flash_attn_bthd_rope_bwd(dop, qr, kr, vp, o2, lse2, cos_f, sin_f)
-        return dq2, rp._rope_qk_bwd(q_empty, dkr, cos_f, sin_f)[1], dvr
-
-    for _ in range(5):
-        step_rope_separate()
-        step_rope_fused()
-    rope_sep_ms = timed(step_rope_separate, args.steps)
-    rope_fused_ms = timed(step_rope_fused, args.steps)
+    rope_us = {}
+    for fused in (False, True):
+        for _ in range(5):
+            rope_flow(fused)
+    for trial in range(3):  # interleaved
+        for fused in (False, True):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            for _ in range(args.steps):
+                rope_flow(fused)
+            e1.record(stream)
+            e1.synchronize()
+            rope_us.setdefault(fused, []).append(e0.elapsed_time(e1) * 1e3 / args.steps)
+    rope_sep_us, rope_fused_us = (statistics.median(rope_us[f]) for f in (False, True))
     qbytes = B * T * H * D * dtype.itemsize
 
     # ---- the RoPE kernel beside the op (q and k in the projection layout, one launch) ----
@@ -901,12 +925,13 @@ def main():
             "bwd_GBps": round(norm["bwd_bytes"] / (norm_us["bwd"] * 1e-6) / 1e9, 1),
         },
         "rope_fusion": {
-            "how": "rope_qk(q, k) + flash_attn_bthd fwd + bwd + rope_qk_bwd(dq, dk), against rope of k alone + "
-            "flash_attn_bthd_rope fwd + bwd (q rotated in the forward's registers, dq rotated back in the dQ kernel) "
-            "+ rope_qk_bwd(dk); torch.library ops back to back, warm caches",
-            "separate_ms_per_step": round(rope_sep_ms, 5),
-            "fused_ms_per_step": round(rope_fused_ms, 5),
-            "saved_us": round((rope_sep_ms - rope_fused_ms) * 1e3, 2),
+            "how": "GPU time of the C-ABI flows back to back (HIP events, median of 3 interleaved runs): nn_rope_qk(q, "
+            "k) + nn_fa_fwd_strided + nn_fa_bwd_strided + nn_rope_qk_bwd(dq, dk), against nn_rope_qk(k) + "
+            "nn_fa_fwd_rope_strided + nn_fa_bwd_rope_strided (q rotated in the forward's registers, dq rotated back "
+            "in the dQ kernel) + nn_rope_qk_bwd(dk)",
+            "separate_us_per_step": round(rope_sep_us, 2),
+            "fused_us_per_step": round(rope_fused_us, 2),
+            "saved_us": round(rope_sep_us - rope_fused_us, 2),
             # the RoPE kernel's read of q (its q_rot write moves into the forward) and rope_qk_bwd's read and
             # write of dq
             "q_trip_bytes_removed": 3 * qbytes,

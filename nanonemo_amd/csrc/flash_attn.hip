@@ -364,37 +364,57 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_kernel(const u16* __restrict__ 
     const int g16 = (lane >> 4) & 1;  // which 16-column half of a 32-wide MFMA tile this lane reads
     const int q0 = qb * BM, qw = q0 + wave * 32, qrow = qw + l32;
 
+    const int ntiles = (min(q0 + BM, T) + BN - 1) / BN;
+    auto issue = [&](int it, u16* kb, u16* vb) {
+        dma_rows<HD, BN, NW>(Kp, lk.st, it * BN, T, kb, wave, dfo);
+        dma_rows<HD, BN, NW>(Vp, lk.st, it * BN, T, vb, wave, dfo);
+    };
     u16x8 qf[NS];
-#pragma unroll
-    for (int s = 0; s < NS; ++s) qf[s] = qrow < T ? ld8(Q + qoff + (size_t)qrow * lq.st + 16 * s + 8 * hh) : u16x8{};
     if constexpr (ROPE) {
+        // Rows past T load row T - 1 (their scores stay finite and nothing of theirs is stored): unconditional
+        // loads, which the compiler keeps in flight together.
+        const int qc = min(qrow, T - 1);
+#pragma unroll
+        for (int s = 0; s < NS; ++s) qf[s] = ld8(Q + qoff + (size_t)qc * lq.st + 16 * s + 8 * hh);
+    } else {
+#pragma unroll
+        for (int s = 0; s < NS; ++s) qf[s] = qrow < T ? ld8(Q + qoff + (size_t)qrow * lq.st + 16 * s + 8 * hh) : u16x8{};
+    }
+    if constexpr (ROPE) {
+        // The row's cos / sin values are loaded with the Q rows and the first K / V tile copy is issued with
+        // them, before the rotation, so that the three latencies overlap. The rotated rows are stored to q_rot
+        // at the end, with O: vector-memory counts complete in order, so a store issued earlier would make the
+        // next tile's wait wait for it.
         // qf[s] holds columns 16 s + 8 hh .. + 7 of the row, so qf[s] and qf[s + NS / 2] are the two halves of
         // the same rotation pairs (columns c and c + HD / 2, c < HD / 2).
-        if (qrow < T) {
-            constexpr int HALF = HD / 2;
-            const float* cr = ra.cosT + (size_t)qrow * HALF;
-            const float* sr = ra.sinT + (size_t)qrow * HALF;
+        constexpr int HALF = HD / 2;
+        f32x4 cs[NS / 2][2], sn[NS / 2][2];
+        const float* cr = ra.cosT + (size_t)min(qrow, T - 1) * HALF;
+        const float* sr = ra.sinT + (size_t)min(qrow, T - 1) * HALF;
+#pragma unroll
+        for (int s = 0; s < NS / 2; ++s)
+#pragma unroll
+            for (int x = 0; x < 2; ++x) {
+                cs[s][x] = *reinterpret_cast<const f32x4*>(cr + 16 * s + 8 * hh + 4 * x);
+                sn[s][x] = *reinterpret_cast<const f32x4*>(sr + 16 * s + 8 * hh + 4 * x);
+            }
+        issue(0, kA, vA);
+        {
 #pragma unroll
             for (int s = 0; s < NS / 2; ++s) {
-                const int c0 = 16 * s + 8 * hh;
-                const f32x4 ca = *reinterpret_cast<const f32x4*>(cr + c0), cb = *reinterpret_cast<const f32x4*>(cr + c0 + 4);
-                const f32x4 sa = *reinterpret_cast<const f32x4*>(sr + c0), sb = *reinterpret_cast<const f32x4*>(sr + c0 + 4);
                 float y1[8], y2[8];
 #pragma unroll
                 for (int j = 0; j < 8; ++j) {
-                    const float cs = j < 4 ? ca[j] : cb[j - 4], sn = j < 4 ? sa[j] : sb[j - 4];
+                    const float c = cs[s][j >> 2][j & 3], si = sn[s][j >> 2][j & 3];
                     const float x1 = E::to_f32(qf[s][j]), x2 = E::to_f32(qf[s + NS / 2][j]);
-                    y1[j] = sub_rn(mul_rn(x1, cs), mul_rn(x2, sn));
-                    y2[j] = add_rn(mul_rn(x1, sn), mul_rn(x2, cs));
+                    y1[j] = sub_rn(mul_rn(x1, c), mul_rn(x2, si));
+                    y2[j] = add_rn(mul_rn(x1, si), mul_rn(x2, c));
                 }
                 const u32x4 w1 = {E::pack2(y1[0], y1[1]), E::pack2(y1[2], y1[3]), E::pack2(y1[4], y1[5]), E::pack2(y1[6], y1[7])};
                 const u32x4 w2 = {E::pack2(y2[0], y2[1]), E::pack2(y2[2], y2[3]), E::pack2(y2[4], y2[5]), E::pack2(y2[6], y2[7])};
                 qf[s] = __builtin_bit_cast(u16x8, w1);
                 qf[s + NS / 2] = __builtin_bit_cast(u16x8, w2);
             }
-            u16* qo = ra.qrot + qoff + (size_t)qrow * lq.st;
-#pragma unroll
-            for (int s = 0; s < NS; ++s) *reinterpret_cast<u16x8*>(qo + 16 * s + 8 * hh) = qf[s];
         }
     }
 
@@ -414,11 +434,6 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_kernel(const u16* __restrict__ 
 #pragma unroll
         for (int x = 0; x < 2; ++x) voff[dt][x] = col_off<HD>(8 * x + 4 * hh, 32 * dt + 16 * g16, lane);
 
-    const int ntiles = (min(q0 + BM, T) + BN - 1) / BN;
-    auto issue = [&](int it, u16* kb, u16* vb) {
-        dma_rows<HD, BN, NW>(Kp, lk.st, it * BN, T, kb, wave, dfo);
-        dma_rows<HD, BN, NW>(Vp, lk.st, it * BN, T, vb, wave, dfo);
-    };
     // One 128-key tile as four 32-key sub-tiles, software-pipelined so that the matrix unit and the
     // VALU have independent work in the same stretch of straight-line code:
     //   * K operands of sub-tile t+2 are read from LDS while sub-tile t is processed, so the S^T
@@ -530,7 +545,7 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_kernel(const u16* __restrict__ 
             tile(std::false_type{}, k0, kb, vb);
     };
 
-    issue(0, kA, vA);
+    if constexpr (!ROPE) issue(0, kA, vA);
     for (int it = 0; it < ntiles; it += 2) {
         wait_vmem();
         __syncthreads();
@@ -545,6 +560,11 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_kernel(const u16* __restrict__ 
 
     const float ltot = pair_sum(lsum);
     if (qrow < T) {
+        if constexpr (ROPE) {  // the rotated rows, stored with O (a store inside the loop would hold up tile waits)
+            u16* qo = ra.qrot + qoff + (size_t)qrow * lq.st;
+#pragma unroll
+            for (int s = 0; s < NS; ++s) *reinterpret_cast<u16x8*>(qo + 16 * s + 8 * hh) = qf[s];
+        }
         const float inv = 1.f / ltot;
         u16* op = O + qoff + (size_t)qrow * lq.st;
 #pragma unroll
