@@ -37,7 +37,7 @@ The JSON line also carries:
                 then the dK/dV kernel) and the HBM rate of the standalone preprocessing entry point;
   layout_fusion the same fwd+bwd from (B, T, heads, hd) projections: through transposed views and the
                 dense ops (the reference model's flow, with its copies) vs the layout-fused
-                nanonemo::flash_attn_bthd ops;
+                nanonemo::flash_attn_bthd ops, with the host's time per step beside each;
   rope_qk       the HIP RoPE kernel on the workload's q and k (projection layout, one launch) and its
                 HBM rate, beside the plain-PyTorch formula;
   add_rmsnorm   the HIP fused residual add + RMSNorm forward and backward (dx, ddelta and dw) on the
@@ -188,8 +188,11 @@ def same_node(q, k, v, do, fa, reps):
     (/root/reference/benchmarks/kernels/flash_attn.py:27-49: SDPA mem-efficient and SDPA math on
     repeat_interleave'd K/V), plus SDPA's flash backend with native GQA (enable_gqa) where this PyTorch has one,
     and this build's op through autograd the same way: fwd + autograd.grad w.r.t. q, k, v, back to back on warm
-    caches, mean time per call from HIP events (host_ms: the host's time per call, which exceeds ms where the
-    host, not the GPU, sets the pace)."""
+    caches; ms: time per call from HIP events, host_ms: the host's time per call in the same loop (where host_ms
+    reaches ms, the host, not the GPU, sets the pace). Neither a spin kernel that holds the device while the host
+    enqueues nor the profiler's kernel records give the device time of a host-paced loop faithfully here: the
+    nearly idle device lowers its clock during a spin (the next milliseconds run up to about 15 % slower), and
+    per-kernel tracing lengthens the kernels."""
     import warnings
 
     import torch
@@ -716,8 +719,18 @@ def main():
             step_views()
             step_fused()
         torch.cuda.synchronize()
+    def host_ms(fn, n):  # the host's time per call in a loop of n calls (device work enqueued, not waited for)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(n):
+            fn()
+        t1 = time.perf_counter()
+        torch.cuda.synchronize()
+        return (t1 - t0) * 1e3 / n
+
     views_ms = timed(step_views, args.steps)
     fused_ms = timed(step_fused, args.steps)
+    views_host_ms, fused_host_ms = host_ms(step_views, args.steps), host_ms(step_fused, args.steps)
 
     # ---- q's RoPE folded into the attention, against the separate RoPE kernel, as GPU time: the C-ABI flows
     # back to back, timed with HIP events on the launch stream (the ops' host cost would set the pace of a loop of
@@ -937,8 +950,9 @@ def main():
             "q_trip_bytes_removed": 3 * qbytes,
         },
         "same_node": {
-            "how": "fwd + autograd.grad back to back, warm caches, HIP events; SDPA as the reference benchmark runs it "
-            "(repeat_interleave'd K/V), flash with native GQA; op_pair = this build's two ops without autograd",
+            "how": "fwd + autograd.grad back to back, warm caches, HIP events (host_ms: the host's time per call in the "
+            "same loop); SDPA as the reference benchmark runs it (repeat_interleave'd K/V), flash with native GQA; "
+            "op_pair = this build's two ops without autograd",
             "this_build_op_pair_ms": round(op_ms, 5),
             **sdpa_cmp,
         },
@@ -947,6 +961,9 @@ def main():
             "views_ms_per_step": round(views_ms, 5),
             "fused_ms_per_step": round(fused_ms, 5),
             "speedup": round(views_ms / fused_ms, 3),
+            # the host's time per step in the same loops: where it reaches the step time, the host sets the pace
+            "views_host_ms_per_step": round(views_host_ms, 5),
+            "fused_host_ms_per_step": round(fused_host_ms, 5),
         },
         "roofline": {
             "kernel": kernel_names[dominant],
