@@ -218,7 +218,7 @@ __global__ __launch_bounds__(64 * kWaves) void add_rmsnorm_fwd_kernel(const void
 // teams of a wave are summed over their lane groups and the block's waves in LDS into partial row
 // blockIdx.x.
 // ------------------------------------------------------------------------------------------
-template <int W, int K, int R, bool DELTA, int NWV>
+template <int W, int K, int R, bool DELTA, int NWV, bool PIPE>
 __global__ __launch_bounds__(64 * NWV) void add_rmsnorm_bwd_kernel(
     const void* __restrict__ dy, const void* __restrict__ dh, const void* __restrict__ h, const float* __restrict__ w,
     const float* __restrict__ rstd, void* __restrict__ dx, void* __restrict__ ddelta, float* __restrict__ dw_part,
@@ -227,6 +227,10 @@ __global__ __launch_bounds__(64 * NWV) void add_rmsnorm_bwd_kernel(
     // Wide rows (more than 32 values per lane) take two passes over the row per team: the first sums g * h and
     // dw, the second re-reads the row (now in cache) for dx, so that only dw stays resident across rows.
     constexpr bool TWO_PASS = W * K > 32;
+    // PIPE: one pass per row, software-pipelined over the team's rows (two rows' values in registers beside dw and
+    // the weight); the host selects it where it measured faster (see bwd_pipelined). Otherwise rows of up to 32
+    // values per lane take one pass, a row at a time.
+    static_assert(!PIPE || W * K <= 24, "two rows of this width do not fit in registers");
     __shared__ float red[NWV][R * W];  // one unit's dw per wave, per lane position
     const int team = threadIdx.x / R, t = threadIdx.x % R, wave = threadIdx.x >> 6;
     const int units = N / W;
@@ -252,7 +256,51 @@ __global__ __launch_bounds__(64 * NWV) void add_rmsnorm_bwd_kernel(
         }
     };
 
-    for (long long row = (long long)blockIdx.x * TPB + team; row < M; row += teams) {
+    if constexpr (PIPE) {
+        // The next row's loads are issued before this row's arithmetic and stores, so that the grid's reads and
+        // writes overlap (the host gives every team at least two rows where the rows allow it).
+        auto fetch = [&](long long rw, Slice<W, K>& g, Slice<W, K>& hv, Slice<W, K>& res, float& r) {
+            const long long off = rw * N;
+            r = rstd[rw];
+            load_slice<W, K, R>((const char*)dy + off * dyb, dydt, t, units, g);
+            load_slice<W, K, R>((const char*)h + off * hb, hdt, t, units, hv);
+            if constexpr (DELTA) load_slice<W, K, R>((const char*)dh + off * hb, hdt, t, units, res);
+        };
+        Slice<W, K> gv, hv, res;  // this row: dy (then g, then the gradient), h, and dh
+        float r = 0.f;
+        long long row = (long long)blockIdx.x * TPB + team;
+        if (row < M) fetch(row, gv, hv, res, r);
+        for (; row < M; row += teams) {
+            Slice<W, K> ng, nh, nres;
+            float nr = 0.f;
+            if (row + teams < M) fetch(row + teams, ng, nh, nres, nr);
+            const long long off = row * N;
+            float s = 0.f;
+#pragma unroll
+            for (int k = 0; k < K; ++k)
+#pragma unroll
+                for (int e = 0; e < W; ++e) {
+                    acc.v[k][e] = fmaf(gv.v[k][e], hv.v[k][e] * r, acc.v[k][e]);  // dw += dy * (h r)
+                    gv.v[k][e] *= wv.v[k][e];                                     // g = dy * w
+                    s = fmaf(gv.v[k][e], hv.v[k][e], s);
+                }
+            const float c = r * r * r * team_sum<R>(s) / (float)N;
+#pragma unroll
+            for (int k = 0; k < K; ++k)
+#pragma unroll
+                for (int e = 0; e < W; ++e) {
+                    const float d = gv.v[k][e] * r - hv.v[k][e] * c;
+                    gv.v[k][e] = DELTA ? d + res.v[k][e] : d;
+                }
+            store_slice<W, K, R>((char*)dx + off * elem_bytes(dxdt), dxdt, t, units, gv);
+            if constexpr (DELTA) store_slice<W, K, R>((char*)ddelta + off * elem_bytes(dddt), dddt, t, units, gv);
+            gv = ng;
+            hv = nh;
+            if constexpr (DELTA) res = nres;
+            r = nr;
+        }
+    }
+    for (long long row = (long long)blockIdx.x * TPB + team; !PIPE && row < M; row += teams) {
         const long long off = row * N;
         const float r = rstd[row];
         if constexpr (TWO_PASS) {
@@ -468,9 +516,21 @@ template <int W, int K>
 constexpr int bwd_waves() { return W * K > 48 ? 4 : kBwdWaves; }
 int bwd_waves_of(const Layout& L) { return L.W * L.K > 48 ? 4 : kBwdWaves; }
 
-// Backward grid: enough blocks for one row per team, at most kBwdBlocks.
+// The pipelined backward, with two rows per team, for rows of three 16-byte vectors per lane (N = 520 .. 768 in
+// 32-lane teams, the 114 M model's width) where two rows per team give 256 to 512 blocks. Measured against a row
+// at a time (interleaved A/B): 22.9 against 27.5 us at 8192 x 768, 40.8 against 43.2 at 16384 x 768; with fewer
+// blocks than CUs, with teams walking more rows (32768 x 768: +2.6 %) or at other widths (8192 x 512: +3 %,
+// 16384 x 512: +9 %) it is slower, and those shapes keep the row-at-a-time kernel.
+constexpr long long kBwdFillBlocks = 256;
+bool bwd_pipelined(long long M, const Layout& L) {
+    const long long per = 64LL * bwd_waves_of(L) / L.R;  // teams per block
+    const long long b2 = (M + 2 * per - 1) / (2 * per);
+    return L.W == 8 && L.K == 3 && b2 >= kBwdFillBlocks && b2 <= kBwdBlocks;
+}
+
+// Backward grid: one row per team (two when pipelined), at most kBwdBlocks blocks, whose teams then walk further rows.
 long long bwd_blocks(long long M, const Layout& L) {
-    const long long per = 64LL * bwd_waves_of(L) / L.R;
+    const long long per = 64LL * bwd_waves_of(L) / L.R * (bwd_pipelined(M, L) ? 2 : 1);
     const long long b = (M + per - 1) / per;
     return b < kBwdBlocks ? b : kBwdBlocks;
 }
@@ -538,13 +598,21 @@ NNRMS_API int nn_add_rmsnorm_bwd(const void* dy, const void* dh, const void* h, 
         !aligned(workspace, 16) || !aligned(dw, 4) || (dh && (!al(dh, h_dtype) || !al(ddelta, ddelta_dtype))))
         return fail("tensors must be 16-byte aligned");
     const long long P = bwd_blocks(M, L);
+    const bool pipe = bwd_pipelined(M, L);
     int rc = with_layout(L, dh != nullptr, [&](auto w_, auto k_, auto r_, auto d_) {
-        constexpr int NWV = bwd_waves<decltype(w_)::value, decltype(k_)::value>();
-        add_rmsnorm_bwd_kernel<decltype(w_)::value, decltype(k_)::value, decltype(r_)::value, decltype(d_)::value, NWV>
-            <<<dim3((unsigned)P), dim3(64 * NWV), 0, st>>>(dy, dh, h, weight, rstd, dx, ddelta, (float*)workspace,
-                                                               (long long)M, (int)N, dy_dtype, h_dtype, dx_dtype,
-                                                               dh ? ddelta_dtype : dx_dtype);
-        return launched("add_rmsnorm_bwd_kernel");
+        constexpr int W = decltype(w_)::value, K = decltype(k_)::value, R = decltype(r_)::value;
+        constexpr bool D = decltype(d_)::value;
+        constexpr int NWV = bwd_waves<W, K>();
+        auto go = [&](auto kern) {
+            kern<<<dim3((unsigned)P), dim3(64 * NWV), 0, st>>>(dy, dh, h, weight, rstd, dx, ddelta, (float*)workspace,
+                                                                (long long)M, (int)N, dy_dtype, h_dtype, dx_dtype,
+                                                                dh ? ddelta_dtype : dx_dtype);
+            return launched("add_rmsnorm_bwd_kernel");
+        };
+        if constexpr (W == 8 && K == 3) {
+            if (pipe) return go(add_rmsnorm_bwd_kernel<W, K, R, D, NWV, true>);
+        }
+        return go(add_rmsnorm_bwd_kernel<W, K, R, D, NWV, false>);
     });
     if (rc) return rc;
     colsum_kernel<<<dim3(cblocks), dim3(64 * kSumWaves), 0, st>>>((const float*)workspace, dw, (int)P, (int)N);
