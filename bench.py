@@ -3,6 +3,7 @@
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--dtype bf16|fp16] [--batch 8] [--seq 1024]
     python bench.py --sweep        # step and per-kernel times over the SWEEP shapes, one JSON line each
     python bench.py --probes       # VALU/MFMA co-issue table and shader clock under load (probe library)
+    python bench.py --timeline     # per-block timelines of the three attention kernels (timeline build)
 
 A step is one forward + backward of the hot path through the drop-in torch.library ops (nanonemo::flash_attn
 then nanonemo::flash_attn_bwd, which call the C ABI of include/nanonemo_fa.h) on synthetic N(0,1) inputs
@@ -266,6 +267,10 @@ def parse():
     p.add_argument("--probes", action="store_true",
                    help="instead of the headline line: the VALU/MFMA co-issue table and the shader clock under load "
                    "(nanonemo_amd/csrc/probe.hip), one JSON line")
+    p.add_argument("--timeline", action="store_true",
+                   help="instead of the headline line: per-block timelines of the forward, dQ and dK/dV kernels at "
+                   "the workload's shape, from libnanonemo_fa_timeline.so, one JSON line")
+    p.add_argument("--timeline-out", default=None, help="with --timeline: also save the raw records (.npz)")
     return p.parse_args()
 
 
@@ -516,8 +521,137 @@ def probes():
     }}), flush=True)
 
 
+def timeline(args):
+    """Per-block timelines of the forward, dQ and dK/dV kernels at the workload's shape, from the timeline build
+    (libnanonemo_fa_timeline.so: the same kernels, each block stamping the 100 MHz constant clock at its start and
+    end and the shader clock at its phase boundaries). The records come from the last of 20 back-to-back
+    fwd + nn_fa_bwd steps after about 1 s of steps. Per kernel: when it ran (µs from the forward's first block),
+    how many blocks ran at once and what fraction of that slot-time held a block, when its first block ended and
+    its last block started, the shader clock over a block, its blocks' phase lengths in shader cycles (forward and
+    dQ: start to first tile ready, dQ's row-load and preprocessing prologue within it; dK/dV: prologue, the
+    spread of the 4 waves' loop ends in a unit, which the slowest sets, and the first unit's reduction), and, for
+    the forward and dQ, per tile count when those blocks started and ended. One JSON line."""
+    import numpy as np
+    import torch
+
+    from nanonemo_amd.build import TIMELINE_LIB
+    from nanonemo_amd.kernels.hip import DTYPE_BF16, DTYPE_F16, SIGNATURES
+
+    if not TIMELINE_LIB.exists():
+        raise RuntimeError(f"{TIMELINE_LIB} is not built; run `python -m nanonemo_amd.build`")
+    TL = ctypes.CDLL(str(TIMELINE_LIB))
+    for name in ("nn_fa_fwd", "nn_fa_bwd", "nn_fa_bwd_workspace_size", "nn_fa_last_error"):
+        fn = getattr(TL, name)
+        fn.restype, fn.argtypes = SIGNATURES[name]
+    TL.nn_fa_timeline_dims.argtypes = [ctypes.POINTER(ctypes.c_int)] * 3
+    TL.nn_fa_timeline_read.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_int]
+
+    def ok(rc):
+        if rc != 0:
+            raise RuntimeError(TL.nn_fa_last_error().decode(errors="replace"))
+
+    nk, nb, nw = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+    ok(TL.nn_fa_timeline_dims(ctypes.byref(nk), ctypes.byref(nb), ctypes.byref(nw)))
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    sp = torch.cuda.current_stream().cuda_stream
+    B, T, H, KVH, D = args.batch, args.seq, args.heads, args.kv_heads, args.head_dim
+    dtype = torch.bfloat16 if args.dtype == "bf16" else torch.float16
+    a = (B, H, KVH, T, D, DTYPE_BF16 if args.dtype == "bf16" else DTYPE_F16, 1.0 / math.sqrt(D), sp)
+    torch.manual_seed(0)
+    q, do = ((torch.randn(B, H, T, D, device=dev) * args.input_scale).to(dtype) for _ in range(2))
+    k, v = ((torch.randn(B, KVH, T, D, device=dev) * args.input_scale).to(dtype) for _ in range(2))
+    o, dq, dk, dv = torch.empty_like(q), torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    lse = torch.empty(B, H, T, dtype=torch.float32, device=dev)
+    wsb = TL.nn_fa_bwd_workspace_size(B, H, KVH, T, D)
+    ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=dev)
+
+    def step():
+        ok(TL.nn_fa_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(), *a))
+        ok(TL.nn_fa_bwd(do.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(),
+                        dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), ws.data_ptr(), wsb, *a))
+
+    for _ in range(max(args.warmup, 3)):
+        step()
+    t_end = time.perf_counter() + args.prewarm
+    while time.perf_counter() < t_end:
+        for _ in range(50):
+            step()
+        torch.cuda.synchronize()
+    ok(TL.nn_fa_timeline_clear())
+    for _ in range(20):
+        step()
+    torch.cuda.synchronize()
+    rec = {}
+    for kern, name in enumerate(("fwd", "dq", "dkdv")):
+        r = np.zeros((nb.value, nw.value), dtype=np.uint64)
+        ok(TL.nn_fa_timeline_read(kern, r.ctypes.data, nb.value))
+        rec[name] = r[r[:, 0] != 0].astype(np.int64)  # blocks of the last launch (a cleared record reads 0)
+    if args.timeline_out:
+        np.savez(args.timeline_out, **rec)
+    t0 = rec["fwd"][:, 0].min()
+    us = lambda ticks: ticks / 100.0  # noqa: E731  (s_memrealtime runs at 100 MHz)
+    rnd = lambda x: round(float(x), 2)  # noqa: E731
+
+    def summary(r, name):
+        start, end = us(r[:, 0] - t0), us(r[:, 1] - t0)
+        ev = sorted([(s_, 1) for s_ in start] + [(e_, -1) for e_ in end], key=lambda x: (x[0], x[1]))
+        live = peak = 0
+        for _, d in ev:
+            live += d
+            peak = max(peak, live)
+        k0, k1 = start.min(), end.max()
+        out = {
+            "blocks": int(len(r)), "start_us": rnd(k0), "end_us": rnd(k1), "span_us": rnd(k1 - k0),
+            "blocks_at_once_max": peak,
+            "slot_time_used": rnd((end - start).sum() / (peak * (k1 - k0))),
+            "first_block_end_us": rnd(end.min() - k0), "last_block_start_us": rnd(start.max() - k0),
+            "shader_mhz_median": round(float(np.median((r[:, 4] - r[:, 2]) / us(r[:, 1] - r[:, 0])))),
+            "blocks_per_xcd": np.bincount((r[:, 5] >> 32) & 0xF, minlength=8).tolist(),
+        }
+        first = start < k0 + 1.0  # the first wave of blocks (started within 1 us of the kernel's start)
+        pro = r[:, 3] - r[:, 2]
+        out["prologue_cycles_median"] = {"first_wave": int(np.median(pro[first])),
+                                         "later": int(np.median(pro[~first])) if (~first).any() else None}
+        if name == "dq":
+            rows = r[:, 6] - r[:, 2]
+            out["row_prologue_cycles_median"] = {"first_wave": int(np.median(rows[first])),
+                                                 "later": int(np.median(rows[~first])) if (~first).any() else None}
+        if name in ("fwd", "dq"):
+            by = {}
+            for nt in sorted(set(r[:, 7].tolist())):
+                m = r[:, 7] == nt
+                by[f"{int(nt)} tiles"] = {
+                    "blocks": int(m.sum()),
+                    "start_us_min_med_max": [rnd(start[m].min() - k0), rnd(np.median(start[m]) - k0),
+                                             rnd(start[m].max() - k0)],
+                    "end_us_min_med_max": [rnd(end[m].min() - k0), rnd(np.median(end[m]) - k0), rnd(end[m].max() - k0)],
+                    "duration_us_median": rnd(np.median(end[m] - start[m])),
+                }
+            out["by_128_key_tiles"] = by
+        if name == "dkdv":
+            loop0, loop1 = r[:, 6:10], r[:, 10:14]
+            out["unit0_loop_end_spread_cycles_median"] = int(np.median(loop0.max(1) - loop0.min(1)))
+            two = (loop1 > 0).all(1)
+            if two.any():
+                out["unit1_loop_end_spread_cycles_median"] = int(np.median(loop1[two].max(1) - loop1[two].min(1)))
+            out["unit0_reduction_cycles_median"] = int(np.median(r[:, 14] - loop0.max(1)))
+            out["block_cycles_median"] = int(np.median(r[:, 4] - r[:, 2]))
+        return out
+
+    print(json.dumps({"timeline": {
+        "workload": {"batch": B, "seq_len": T, "heads": H, "kv_heads": KVH, "head_dim": D, "dtype": args.dtype},
+        "how": "last of 20 back-to-back fwd + nn_fa_bwd steps from libnanonemo_fa_timeline.so; times in us from "
+               "the forward's first block start (100 MHz clock), cycles in shader clocks",
+        **{n: summary(r, n) for n, r in rec.items()},
+    }}), flush=True)
+
+
 def main():
     args = parse()
+    if args.timeline and args.gpus == 1:
+        timeline(args)
+        return
     if args.sweep and args.gpus == 1:
         sweep(args)
         return

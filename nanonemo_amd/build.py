@@ -27,6 +27,10 @@ LIB = LIB_DIR / "libnanonemo_fa.so"
 # the attention library's ABI stays what include/*.h declares.
 PROBE_SRCS = [PKG / "csrc" / "probe.hip"]
 PROBE_LIB = LIB_DIR / "libnanonemo_probe.so"
+# Block timelines for `bench.py --timeline`: the attention kernels built with NN_TIMELINE=1, so that every block
+# records clock stamps at its phase boundaries (the product library compiles those stamps to nothing).
+TIMELINE_SRCS = [PKG / "csrc" / "flash_attn.hip"]
+TIMELINE_LIB = LIB_DIR / "libnanonemo_fa_timeline.so"
 ARCH = "gfx950"
 
 # -packed-fp32-ops: keep v_pk_{add,mul,fma}_f32 out of the generated code (those packed forms have
@@ -62,17 +66,22 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found (looked at $HIPCC, /opt/rocm/bin/hipcc and PATH)")
 
 
-def _compile(srcs: list[Path], lib: Path, verbose: bool) -> Path:
+def _start(srcs: list[Path], lib: Path, verbose: bool, defines: tuple[str, ...] = ()):
     LIB_DIR.mkdir(parents=True, exist_ok=True)
     tmp = lib.with_suffix(".so.tmp")
-    cmd = [hipcc(), *HIPCC_FLAGS, f"-I{ROOT / 'include'}", "-o", str(tmp), *(str(s) for s in srcs)]
+    cmd = [hipcc(), *HIPCC_FLAGS, *defines, f"-I{ROOT / 'include'}", "-o", str(tmp), *(str(s) for s in srcs)]
     if verbose:
         print(" ".join(cmd), flush=True)
-    res = subprocess.run(cmd, capture_output=True, text=True)
+    return subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True), tmp, lib
+
+
+def _finish(job, verbose: bool) -> Path:
+    proc, tmp, lib = job
+    out, _ = proc.communicate()
     noise = "'-packed-fp32-ops' is not a recognized feature"
-    log = "\n".join(l for l in (res.stdout + res.stderr).splitlines() if noise not in l)
-    if res.returncode != 0:
-        raise RuntimeError(f"hipcc failed ({res.returncode}):\n{log}")
+    log = "\n".join(l for l in out.splitlines() if noise not in l)
+    if proc.returncode != 0:
+        raise RuntimeError(f"hipcc failed for {lib.name} ({proc.returncode}):\n{log}")
     if verbose and log.strip():
         print(log, flush=True)
     os.replace(tmp, lib)  # atomic: a process that already mapped the old file keeps it
@@ -80,9 +89,19 @@ def _compile(srcs: list[Path], lib: Path, verbose: bool) -> Path:
 
 
 def build(verbose: bool = False) -> Path:
-    """Compile the HIP library and the measurement probes (always recompiles); return the library's path."""
-    _compile(PROBE_SRCS, PROBE_LIB, verbose)
-    return _compile(SRCS, LIB, verbose)
+    """Compile the HIP library, the measurement probes and the timeline build of the attention kernels, in
+    parallel (always recompiles); return the library's path."""
+    jobs = [_start(SRCS, LIB, verbose), _start(PROBE_SRCS, PROBE_LIB, verbose),
+            _start(TIMELINE_SRCS, TIMELINE_LIB, verbose, ("-DNN_TIMELINE=1",))]
+    errors = []
+    for job in jobs:
+        try:
+            _finish(job, verbose)
+        except RuntimeError as e:
+            errors.append(str(e))
+    if errors:
+        raise RuntimeError("\n".join(errors))
+    return LIB
 
 
 if __name__ == "__main__":

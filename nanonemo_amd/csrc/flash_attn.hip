@@ -66,6 +66,53 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
+// Block timelines, in diagnostic builds only (NN_TIMELINE=1: libnanonemo_fa_timeline.so, which
+// `bench.py --timeline` loads; in the product library every stamp compiles to nothing). One lane records
+// clock readings into a file-scope device array, one record of kTlWords 64-bit words per (kernel, block):
+// the 100 MHz constant clock (s_memrealtime) at the block's start and end, comparable across CUs, the
+// shader clock (s_memtime) at its phase boundaries, for cycle counts within the block, and the XCD and
+// hardware id of the wave that ran it. Block-level words come from wave 0; per-wave words from each wave.
+#ifndef NN_TIMELINE
+#define NN_TIMELINE 0
+#endif
+enum TlKernel { kTlFwd = 0, kTlDq = 1, kTlDkdv = 2, kTlKernels = 3 };
+// Words of a record. Forward and dQ: kTlExtra = dQ's prologue end (rows loaded, -D and -lse/scale
+// written), kTlExtra + 1 = the block's count of 128-key tiles. dK/dV: kTlExtra + 4 u + w = wave w's loop
+// end in the block's unit u (0, 1); kTlExtra + 8 = wave 0 after the first unit's reduction.
+enum TlWord { kTlRtStart = 0, kTlRtEnd = 1, kTlMtStart = 2, kTlMtReady = 3, kTlMtEnd = 4, kTlHw = 5, kTlExtra = 6 };
+constexpr int kTlBlocks = 16384, kTlWords = 16;
+#if NN_TIMELINE
+__device__ __align__(256) unsigned long long nn_timeline[kTlKernels * kTlBlocks * kTlWords];
+__device__ __forceinline__ void tl_word(int kern, int word, unsigned long long v) {
+    if (blockIdx.x < kTlBlocks) nn_timeline[((size_t)kern * kTlBlocks + blockIdx.x) * kTlWords + word] = v;
+}
+__device__ __forceinline__ unsigned long long tl_hw() {
+    // HW_REG_XCC_ID (20), bits 3:0, and HW_REG_HW_ID (4), all 32 bits (CU id in bits 11:8, SE id in 15:13).
+    const unsigned xcc = __builtin_amdgcn_s_getreg((3 << 11) | 20), hw = __builtin_amdgcn_s_getreg((31 << 11) | 4);
+    return ((unsigned long long)xcc << 32) | hw;
+}
+#define NN_TL_BLOCK(kern, word, expr) \
+    do { if (threadIdx.x == 0) tl_word(kern, word, (expr)); } while (0)
+#define NN_TL_WAVE(kern, word, expr) \
+    do { if ((threadIdx.x & 63) == 0) tl_word(kern, word, (expr)); } while (0)
+#define NN_TL_START(kern)                                                                 \
+    do {                                                                                  \
+        NN_TL_BLOCK(kern, kTlRtStart, __builtin_amdgcn_s_memrealtime());                  \
+        NN_TL_BLOCK(kern, kTlMtStart, __builtin_amdgcn_s_memtime());                      \
+        NN_TL_BLOCK(kern, kTlHw, tl_hw());                                                \
+    } while (0)
+#define NN_TL_END(kern)                                                                   \
+    do {                                                                                  \
+        NN_TL_BLOCK(kern, kTlMtEnd, __builtin_amdgcn_s_memtime());                        \
+        NN_TL_BLOCK(kern, kTlRtEnd, __builtin_amdgcn_s_memrealtime());                    \
+    } while (0)
+#else
+#define NN_TL_BLOCK(kern, word, expr) ((void)0)
+#define NN_TL_WAVE(kern, word, expr) ((void)0)
+#define NN_TL_START(kern) ((void)0)
+#define NN_TL_END(kern) ((void)0)
+#endif
+
 constexpr int kF16 = 0;
 constexpr int kBF16 = 1;
 constexpr float kLog2e = 1.4426950408889634f;
@@ -339,6 +386,7 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_kernel(const u16* __restrict__ 
                                                         float* __restrict__ LSE, int BH, int H, int KVH, int T,
                                                         int nqb, float sl2, Lay lq, Lay lk, RopeArgs ra) {
     using E = Elem<DT>;
+    NN_TL_START(kTlFwd);
     constexpr int BM = 128, BN = 128, NW = 4;
     constexpr int NS = HD / 16;  // k-steps of Q K^T
     constexpr int ND = HD / 32;  // 32-wide head_dim tiles of O^T
@@ -365,6 +413,7 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_kernel(const u16* __restrict__ 
     const int q0 = qb * BM, qw = q0 + wave * 32, qrow = qw + l32;
 
     const int ntiles = (min(q0 + BM, T) + BN - 1) / BN;
+    NN_TL_BLOCK(kTlFwd, kTlExtra + 1, (unsigned long long)ntiles);
     auto issue = [&](int it, u16* kb, u16* vb) {
         dma_rows<HD, BN, NW>(Kp, lk.st, it * BN, T, kb, wave, dfo);
         dma_rows<HD, BN, NW>(Vp, lk.st, it * BN, T, vb, wave, dfo);
@@ -549,6 +598,7 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_kernel(const u16* __restrict__ 
     for (int it = 0; it < ntiles; it += 2) {
         wait_vmem();
         __syncthreads();
+        if (it == 0) NN_TL_BLOCK(kTlFwd, kTlMtReady, __builtin_amdgcn_s_memtime());
         if (it + 1 < ntiles) issue(it + 1, kB, vB);
         step(it, kA, vA);
         if (it + 1 >= ntiles) break;
@@ -577,6 +627,7 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_kernel(const u16* __restrict__ 
             }
         if (hh == 0) LSE[(size_t)bh * T + qrow] = (mb + fast_log2(ltot)) * kLn2;
     }
+    NN_TL_END(kTlFwd);
 }
 
 // ------------------------------------------------------------------------------------------
@@ -637,6 +688,7 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(
     int BKV, int H, int KVH, int T, int nkb, int nqt, float sl2, float scale, Lay lq, Lay lk, int nsplit,
     float* __restrict__ part) {
     using E = Elem<DT>;
+    NN_TL_START(kTlDkdv);
     constexpr int BNK = 64, BM = 64, NW = 4, NSL = BNK / 32;
     constexpr int PPB = NW / WPP;  // unit pairs per block: waves WPP p .. WPP p + WPP - 1 share pair p
     static_assert(WPP == 1 || WPP == 2 || WPP == 4, "waves per unit pair");
@@ -879,6 +931,7 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(
         for (int j = 0; j < nmine; j += 2) {  // iteration ifirst + wp is already in flight into buffer A
             const int itn = ifirst + wp + WPP * j;
             wait_vmem();  // this iteration's tiles, copied during the previous one
+            if (ui == 0 && j == 0) NN_TL_BLOCK(kTlDkdv, kTlMtReady, __builtin_amdgcn_s_memtime());
             if (j + 1 < nmine)
                 run(std::true_type{}, itn, qA, oA, lA, itn + WPP, qB, oB, lB);
             else
@@ -895,6 +948,7 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(
         // its K / V registers are free: it issues the next unit's K / V loads and first tiles (into its A
         // slots) now, while it waits for the slower waves, and they stay in flight through the reduction,
         // which uses only the B buffers. The next unit's loop waits for them (vmcnt) before reading either.
+        if (ui < 2) NN_TL_WAVE(kTlDkdv, kTlExtra + 4 * ui + wave, __builtin_amdgcn_s_memtime());
         if (ui + 1 < nunits && active) {
             const int un = nkb - 1 - pj;
             load_kv(un * BNK);
@@ -991,7 +1045,9 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(
             }
             if constexpr (WPP > 1) barrier_lds();  // the B buffers are free for the next unit
         }
+        if (ui == 0) NN_TL_BLOCK(kTlDkdv, kTlExtra + 8, __builtin_amdgcn_s_memtime());
     }
+    NN_TL_END(kTlDkdv);
 }
 
 // ------------------------------------------------------------------------------------------
@@ -1038,6 +1094,7 @@ __global__ __launch_bounds__(256, 2) void fa_bwd_dq_kernel(const u16* __restrict
                                                            u16* __restrict__ dQ, int BH, int H, int KVH, int T, int nqb,
                                                            float sl2, float scale, Lay lq, Lay lk, RopeArgs ra) {
     using E = Elem<DT>;
+    NN_TL_START(kTlDq);
     // LDS tiles of BT = 128 keys (one barrier and one tile wait per 128 keys), each processed as two BN = 64-key
     // halves (the register working set of a 64-key step).
     constexpr int BM = 128, BN = 64, NW = 4, BT = 128;
@@ -1086,6 +1143,7 @@ __global__ __launch_bounds__(256, 2) void fa_bwd_dq_kernel(const u16* __restrict
         nDvec[(size_t)bh * T + qrow] = nd;
         nLvec[(size_t)bh * T + qrow] = -lse / scale;
     }
+    NN_TL_BLOCK(kTlDq, kTlExtra, __builtin_amdgcn_s_memtime());
 
     int koff[NS], kcol[ND][2];
 #pragma unroll
@@ -1100,6 +1158,7 @@ __global__ __launch_bounds__(256, 2) void fa_bwd_dq_kernel(const u16* __restrict
     for (int dt = 0; dt < ND; ++dt) dq[dt] = f32x16{};
 
     const int ntiles = (min(q0 + BM, T) + BT - 1) / BT;
+    NN_TL_BLOCK(kTlDq, kTlExtra + 1, (unsigned long long)ntiles);
     auto issue = [&](int it, u16* kb, u16* vb) {
         dma_rows<HD, BT, NW>(Kp, lk.st, it * BT, T, kb, wave, dfo);
         dma_rows<HD, BT, NW>(Vp, lk.st, it * BT, T, vb, wave, dfo);
@@ -1170,6 +1229,7 @@ __global__ __launch_bounds__(256, 2) void fa_bwd_dq_kernel(const u16* __restrict
     for (int it = 0; it < ntiles; it += 2) {
         wait_vmem();
         __syncthreads();
+        if (it == 0) NN_TL_BLOCK(kTlDq, kTlMtReady, __builtin_amdgcn_s_memtime());
         if (it + 1 < ntiles) issue(it + 1, kB, vB);
         step(it, kA, vA);
         if (it + 1 >= ntiles) break;
@@ -1225,6 +1285,7 @@ __global__ __launch_bounds__(256, 2) void fa_bwd_dq_kernel(const u16* __restrict
                 }
         }
     }
+    NN_TL_END(kTlDq);
 }
 
 // ------------------------------------------------------------------------------------------
@@ -1684,3 +1745,53 @@ NNFA_API int nn_fa_bwd_noalloc(const void* dO, const void* q, const void* k, con
     return bwd_entry(dO, q, k, v, o, lse, dq, dk, dv, ws, kNoAllocScratchBytes, B, H, KVH, T, D, dtype, scale, nullptr,
                      nullptr, stream);
 }
+
+#if NN_TIMELINE
+// ------------------------------------------------------------------------------------------
+// Diagnostic build only: access to the block timelines (see NN_TL_START). Not part of the C ABI in
+// include/nanonemo_fa.h; bench.py --timeline is the one caller. Both functions synchronise the device.
+// ------------------------------------------------------------------------------------------
+namespace {
+int timeline_ptr(unsigned long long** out) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(nn_timeline));
+    if (e != hipSuccess || !p)
+        return fail(e != hipSuccess ? (int)e : -1, "hipGetSymbolAddress(nn_timeline) failed: %s", hipGetErrorString(e));
+    *out = static_cast<unsigned long long*>(p);
+    return 0;
+}
+}  // namespace
+
+// Record layout: kTlKernels kernels x kTlBlocks blocks x kTlWords words (see TlWord).
+NNFA_API int nn_fa_timeline_dims(int* kernels, int* blocks, int* words) {
+    *kernels = kTlKernels;
+    *blocks = kTlBlocks;
+    *words = kTlWords;
+    return 0;
+}
+
+// Zero every record on the current device.
+NNFA_API int nn_fa_timeline_clear(void) {
+    g_last_error.clear();
+    unsigned long long* p = nullptr;
+    if (int e = timeline_ptr(&p)) return e;
+    hipError_t e = hipDeviceSynchronize();
+    if (e == hipSuccess) e = hipMemset(p, 0, sizeof(unsigned long long) * kTlKernels * kTlBlocks * kTlWords);
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    return e == hipSuccess ? 0 : fail((int)e, "timeline clear failed: %s", hipGetErrorString(e));
+}
+
+// Copy the records of kernel `kernel` (a TlKernel), blocks 0 .. nblocks - 1, to host memory `out`.
+NNFA_API int nn_fa_timeline_read(int kernel, unsigned long long* out, int nblocks) {
+    g_last_error.clear();
+    if (kernel < 0 || kernel >= kTlKernels || nblocks < 0 || nblocks > kTlBlocks || !out)
+        return fail(-1, "nn_fa_timeline_read: invalid arguments");
+    unsigned long long* p = nullptr;
+    if (int e = timeline_ptr(&p)) return e;
+    hipError_t e = hipDeviceSynchronize();
+    if (e == hipSuccess)
+        e = hipMemcpy(out, p + (size_t)kernel * kTlBlocks * kTlWords, sizeof(unsigned long long) * nblocks * kTlWords,
+                      hipMemcpyDeviceToHost);
+    return e == hipSuccess ? 0 : fail((int)e, "timeline read failed: %s", hipGetErrorString(e));
+}
+#endif

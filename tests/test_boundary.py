@@ -60,6 +60,31 @@ def test_probe_library_is_separate_and_rejects_bad_arguments():
     assert P.nn_probe_clock(0, 1, 10, None, 16, None) != 0 and b"invalid" in P.nn_probe_last_error()
 
 
+def test_timeline_build_is_separate_and_rejects_bad_arguments():
+    # bench.py --timeline's library is the attention library built with NN_TIMELINE=1: it exports the same
+    # attention entry points plus nn_fa_timeline_*, which the product library does not have; its record read
+    # refuses arguments outside the record array before any device call.
+    from nanonemo_amd.build import TIMELINE_LIB
+
+    assert TIMELINE_LIB.exists(), "run `python -m nanonemo_amd.build` first"
+    TL = ctypes.CDLL(str(TIMELINE_LIB))
+    for name in ("nn_fa_timeline_dims", "nn_fa_timeline_clear", "nn_fa_timeline_read"):
+        assert hasattr(TL, name) and not hasattr(lib(), name), name
+    for name in _declared_symbols():
+        if name.startswith("nn_fa_"):
+            assert hasattr(TL, name), f"{name} missing from the timeline build"
+    dims = [ctypes.c_int() for _ in range(3)]
+    TL.nn_fa_timeline_dims.argtypes = [ctypes.POINTER(ctypes.c_int)] * 3
+    assert TL.nn_fa_timeline_dims(*(ctypes.byref(d) for d in dims)) == 0
+    assert [d.value for d in dims] == [3, 16384, 16]
+    TL.nn_fa_timeline_read.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_int]
+    TL.nn_fa_last_error.restype = ctypes.c_char_p
+    buf = (ctypes.c_uint64 * 16)()
+    for kern, n in ((3, 1), (-1, 1), (0, 16385), (0, -1)):
+        assert TL.nn_fa_timeline_read(kern, buf, n) != 0 and b"invalid" in TL.nn_fa_last_error()
+    assert TL.nn_fa_timeline_read(0, None, 1) != 0
+
+
 def _dkdv_split(B, H, KVH, T):
     """Blocks sharing one dK/dV unit pair: 1 when the B*KVH*ceil(nkb/2) pairs fill 256 CUs, else up to 16,
     keeping at least 8 of a pair's (H/KVH)*(nkb+1) iterations per split, and none where 16 times a unit's
