@@ -516,7 +516,7 @@ template <int W, int K>
 constexpr int bwd_waves() { return W * K > 48 ? 4 : kBwdWaves; }
 int bwd_waves_of(const Layout& L) { return L.W * L.K > 48 ? 4 : kBwdWaves; }
 
-// The pipelined backward, with two rows per team, for rows of three 16-byte vectors per lane (N = 520 .. 768 in
+// The pipelined backward, with two rows per team, for rows of three 8-element units per lane (N = 520 .. 768 in
 // 32-lane teams, the 114 M model's width) where two rows per team give 256 to 512 blocks. Measured against a row
 // at a time (interleaved A/B): 22.9 against 27.5 us at 8192 x 768, 40.8 against 43.2 at 16384 x 768; with fewer
 // blocks than CUs, with teams walking more rows (32768 x 768: +2.6 %) or at other widths (8192 x 512: +3 %,
