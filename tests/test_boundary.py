@@ -217,9 +217,10 @@ def test_rmsnorm_c_abi_backward_checks_and_workspace():
     L = lib()
     # one fp32 dw row per block: a block of 8 waves has 16 teams (32-lane teams) for N <= 1024 with N % 8 == 0,
     # else 8 (64-lane teams); above 3072 (more than 48 values per lane) a block has 4 waves and 4 teams. One row per
-    # team, or two for 3 vectors per lane (the pipelined kernel) where that gives 256 to 512 blocks; at most 512
-    # blocks, whose teams then walk further rows
+    # team, or two for 3 units of 8 elements per lane (the pipelined kernel) where that gives 256 to 512 blocks; at
+    # most 512 blocks, whose teams then walk further rows
     assert L.nn_add_rmsnorm_bwd_workspace_size(8192, 768) == 256 * 768 * 4
+    assert L.nn_add_rmsnorm_bwd_workspace_size(16384, 768) == 512 * 768 * 4  # pipelined, the top of its range
     assert L.nn_add_rmsnorm_bwd_workspace_size(7, 768) == 1 * 768 * 4
     assert L.nn_add_rmsnorm_bwd_workspace_size(7, 4096) == 2 * 4096 * 4
     assert L.nn_add_rmsnorm_bwd_workspace_size(7, 3072) == 1 * 3072 * 4

@@ -3,9 +3,9 @@
 Mirrors the reference's kernel test (/root/reference/tests/kernels/test_rmsnorm.py): its SHAPES and
 dtype pairs, with and without delta, upstream gradients into both outputs (as in the model: the next
 sublayer and the residual stream), the autocast output dtype, opcheck and torch.compile(fullgraph=True).
-Adds: bfloat16 pairs, the 114 M model's full-size shape, a ragged row count for the backward pipelined over two
-rows per team (12289 x 768: the last block's teams hold one row or none), a width just past the two-rows-per-wave
-backward (2056), and the empty input.
+Adds: bfloat16 pairs; the backward pipelined over two rows per team at both ends of its grid range (8192 x 768, the
+114 M model's full-size shape, 256 blocks; 16384 x 768, 512 blocks) and at a ragged row count (12289 x 768: the last
+block's teams hold one row or none); a width just past the two-rows-per-wave backward (2056); and the empty input.
 The oracle sees the same rounded inputs and the residual as the kernel stores it; tolerances are the
 reference's (fp32 1e-5; fp16 rtol 1e-3, atol 4e-3, i.e. 2 ulps at magnitude 2-4), with bf16 at the same
 two ulps of its own precision.
@@ -21,7 +21,8 @@ from oracle import rmsnorm as R
 pytestmark = pytest.mark.gpu
 
 EPS = 1e-5
-SHAPES = [(2048, 768), (7, 768), (1, 33), (130, 1000), (64, 4096), (8192, 768), (12289, 768), (3, 2056), (520, 768)]
+SHAPES = [(2048, 768), (7, 768), (1, 33), (130, 1000), (64, 4096), (8192, 768), (12289, 768), (16384, 768), (3, 2056),
+          (520, 768)]
 DTYPES = [
     (torch.float32, torch.float32),
     (torch.float32, torch.float16),
