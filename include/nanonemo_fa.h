@@ -139,9 +139,11 @@ int nn_fa_bwd_dq(const void* q, const void* k, const void* v, const void* o, con
  * counterpart in the reference: it is for callers that cannot allocate (code under HIP-graph capture,
  * tight serving loops, harnesses that forbid hipMalloc). Shapes whose nn_fa_bwd_workspace_size exceeds
  * 32 MiB (33554432 bytes; e.g. B * H * T above 4M query rows) are rejected with an error. The current
- * device must own `stream`; the first call on a device looks the array up (hipGetSymbolAddress), no call
- * allocates or frees. Calls that overlap on one GPU (other streams or threads) share the array and race;
- * calls in one stream's order do not. */
+ * device must own `stream`; the first call on a device looks the array up (hipGetSymbolAddress, which may
+ * load the library's code object), no call allocates or frees. Code that captures it into a HIP graph
+ * makes one non-empty call on that device before the capture begins (an empty call, B = 0 or T = 0,
+ * returns before the lookup). Calls that overlap on one GPU (other streams or threads) share the array
+ * and race; calls in one stream's order do not. */
 int nn_fa_bwd_noalloc(const void* dO, const void* q, const void* k, const void* v, const void* o,
                       const float* lse, void* dq, void* dk, void* dv,
                       int64_t B, int64_t H, int64_t KVH, int64_t T, int64_t D,

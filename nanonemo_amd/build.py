@@ -23,10 +23,6 @@ ROOT = PKG.parent
 SRCS = [PKG / "csrc" / "flash_attn.hip", PKG / "csrc" / "rope.hip", PKG / "csrc" / "rmsnorm.hip"]
 LIB_DIR = PKG / "lib"
 LIB = LIB_DIR / "libnanonemo_fa.so"
-# Measurement probes for `bench.py --probes` (VALU/MFMA co-issue, shader clock), a library of their own so that
-# the attention library's ABI stays what include/*.h declares.
-PROBE_SRCS = [PKG / "csrc" / "probe.hip"]
-PROBE_LIB = LIB_DIR / "libnanonemo_probe.so"
 # Block timelines for `bench.py --timeline`: the attention kernels built with NN_TIMELINE=1, so that every block
 # records clock stamps at its phase boundaries (the product library compiles those stamps to nothing).
 TIMELINE_SRCS = [PKG / "csrc" / "flash_attn.hip"]
@@ -89,10 +85,9 @@ def _finish(job, verbose: bool) -> Path:
 
 
 def build(verbose: bool = False) -> Path:
-    """Compile the HIP library, the measurement probes and the timeline build of the attention kernels, in
-    parallel (always recompiles); return the library's path."""
-    jobs = [_start(SRCS, LIB, verbose), _start(PROBE_SRCS, PROBE_LIB, verbose),
-            _start(TIMELINE_SRCS, TIMELINE_LIB, verbose, ("-DNN_TIMELINE=1",))]
+    """Compile the HIP library and the timeline build of the attention kernels, in parallel (always
+    recompiles); return the library's path."""
+    jobs = [_start(SRCS, LIB, verbose), _start(TIMELINE_SRCS, TIMELINE_LIB, verbose, ("-DNN_TIMELINE=1",))]
     errors = []
     for job in jobs:
         try:

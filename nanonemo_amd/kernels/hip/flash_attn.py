@@ -63,6 +63,33 @@ def _contig(t: Tensor) -> Tensor:
     return t if t.is_contiguous() else t.contiguous()
 
 
+_CAPTURE_MSG = (
+    "{}: capturing this op into a HIP graph while autograd records it (torch.cuda.graph around the forward and its "
+    "autograd backward, or torch.compile(mode='reduce-overhead')) is not supported: such a capture once ended in a "
+    "host fault in capture_end and no cause has been shown. Capture the C ABI calls (nn_fa_fwd / nn_fa_bwd / "
+    "nn_fa_bwd_noalloc) instead, or run the ops eagerly (torch.compile(fullgraph=True) without graphs is supported)."
+)
+
+
+def _refuse_capture_with_autograd(where: str, *inputs: Tensor) -> None:
+    """Raise when the current stream is capturing and autograd will record this op: before any launch in the
+    public functions (grad mode on and an input requires grad), and in setup_context / the backward as a
+    backstop for direct op calls. Capture without autograd, and capture of the C ABI, are unaffected. Skipped
+    while torch.compile traces (the check is a host query, and no capture runs at trace time)."""
+    if inputs and not (torch.is_grad_enabled() and any(t.requires_grad for t in inputs)):
+        return
+    if torch.compiler.is_compiling() or not (torch.cuda.is_available() and torch.cuda.is_current_stream_capturing()):
+        return
+    raise RuntimeError(_CAPTURE_MSG.format(where))
+
+
+def _refuse_capture_from_autograd_engine(where: str) -> None:
+    """In the backward ops' bodies: raise when the autograd engine runs them (directly, or inside a compiled
+    backward such as torch.compile's mode='reduce-overhead' records) while the current stream is capturing."""
+    if torch._C._current_autograd_node() is not None:
+        _refuse_capture_with_autograd(where)
+
+
 @torch.library.custom_op("nanonemo::flash_attn", mutates_args=())
 def _flash_attn(q: Tensor, k: Tensor, v: Tensor) -> tuple[Tensor, Tensor]:
     q, k, v = _contig(q), _contig(k), _contig(v)
@@ -100,6 +127,7 @@ def _flash_attn_bwd(d_o: Tensor, q: Tensor, k: Tensor, v: Tensor, o: Tensor, lse
     KVH = k.size(1)
     if lse.shape != (B, H, T) or lse.dtype != torch.float32:
         raise RuntimeError("lse must be a float32 tensor of shape (B, H, T)")
+    _refuse_capture_from_autograd_engine("flash_attn backward op")
     dq = torch.empty_like(q, memory_format=torch.contiguous_format)
     dk = torch.empty_like(k, memory_format=torch.contiguous_format)
     dv = torch.empty_like(v, memory_format=torch.contiguous_format)
@@ -124,6 +152,7 @@ def _(d_o, q, k, v, o, lse):
 
 
 def _setup_context(ctx, inputs, output):
+    _refuse_capture_with_autograd("flash_attn (autograd)")
     q, k, v = inputs
     o, lse = output
     ctx.save_for_backward(q, k, v, o, lse)
@@ -137,6 +166,7 @@ def _d_out(d_o, o):
 
 
 def _backward(ctx, d_o, _d_lse):
+    _refuse_capture_with_autograd("flash_attn backward")
     q, k, v, o, lse = ctx.saved_tensors
     return _flash_attn_bwd(_d_out(d_o, o), q, k, v, o, lse)
 
@@ -146,6 +176,7 @@ _flash_attn.register_autograd(_backward, setup_context=_setup_context)
 
 def flash_attn(q: Tensor, k: Tensor, v: Tensor) -> Tensor:
     """Causal GQA attention. q: (B, H, T, hd), k/v: (B, KVH, T, hd), fp16 or bf16, H % KVH == 0, hd in {32, 64}."""
+    _refuse_capture_with_autograd("flash_attn", q, k, v)
     o, _ = _flash_attn(q, k, v)
     return o
 
@@ -206,6 +237,7 @@ def _flash_attn_bthd_bwd(
     KVH = k.size(2)
     if lse.shape != (B, H, T) or lse.dtype != torch.float32:
         raise RuntimeError("lse must be a float32 tensor of shape (B, H, T)")
+    _refuse_capture_from_autograd_engine("flash_attn_bthd backward op")
     dq = torch.empty_like(q, memory_format=torch.contiguous_format)
     dk = torch.empty_like(k, memory_format=torch.contiguous_format)
     dv = torch.empty_like(v, memory_format=torch.contiguous_format)
@@ -230,6 +262,7 @@ def _(d_o, q, k, v, o, lse):
 
 
 def _backward_bthd(ctx, d_o, _d_lse):
+    _refuse_capture_with_autograd("flash_attn_bthd backward")
     q, k, v, o, lse = ctx.saved_tensors
     return _flash_attn_bthd_bwd(_d_out(d_o, o), q, k, v, o, lse)
 
@@ -239,6 +272,7 @@ _flash_attn_bthd.register_autograd(_backward_bthd, setup_context=_setup_context)
 
 def flash_attn_bthd(q: Tensor, k: Tensor, v: Tensor) -> Tensor:
     """Causal GQA attention in the projection layout: q (B, T, H, hd), k/v (B, T, KVH, hd) -> o (B, T, H, hd)."""
+    _refuse_capture_with_autograd("flash_attn_bthd", q, k, v)
     o, _ = _flash_attn_bthd(q, k, v)
     return o
 
@@ -253,9 +287,13 @@ def flash_attn_bthd(q: Tensor, k: Tensor, v: Tensor) -> Tensor:
 # output are not propagated (the model uses neither), as the reference ignores lse's.
 
 
-def _check_tables(cos: Tensor, sin: Tensor, T: int, D: int) -> tuple[Tensor, Tensor]:
+def _check_tables(cos: Tensor, sin: Tensor, T: int, D: int, device: torch.device) -> tuple[Tensor, Tensor]:
+    """The RoPE tables: float32 (T_max >= T, hd/2), on the inputs' GPU. Checked before any launch, since the
+    library reads them through raw device pointers (a host table would be read as device memory)."""
+    if not (cos.is_cuda and sin.is_cuda) or cos.device != device or sin.device != device:
+        raise RuntimeError("cos/sin must be float32 (T_max >= T, hd/2) tables on the inputs' device")
     if cos.dtype != torch.float32 or sin.dtype != torch.float32 or cos.shape != sin.shape or cos.dim() != 2 \
-            or cos.shape[1] != D // 2 or cos.shape[0] < T or cos.device != sin.device:
+            or cos.shape[1] != D // 2 or cos.shape[0] < T:
         raise RuntimeError("cos/sin must be float32 (T_max >= T, hd/2) tables on the inputs' device")
     return _contig(cos), _contig(sin)
 
@@ -266,7 +304,7 @@ def _flash_attn_bthd_rope(q: Tensor, k: Tensor, v: Tensor, cos: Tensor, sin: Ten
     _check_inputs(q, k, v, seq_dim=1)
     B, T, H, D = q.shape
     KVH = k.size(2)
-    cos, sin = _check_tables(cos, sin, T, D)
+    cos, sin = _check_tables(cos, sin, T, D, q.device)
     o = torch.empty_like(q, memory_format=torch.contiguous_format)
     q_rot = torch.empty_like(q, memory_format=torch.contiguous_format)
     lse = torch.empty((B, H, T), dtype=torch.float32, device=q.device)
@@ -304,7 +342,8 @@ def _flash_attn_bthd_rope_bwd(
     KVH = k.size(2)
     if lse.shape != (B, H, T) or lse.dtype != torch.float32:
         raise RuntimeError("lse must be a float32 tensor of shape (B, H, T)")
-    cos, sin = _check_tables(cos, sin, T, D)
+    _refuse_capture_from_autograd_engine("flash_attn_bthd_rope backward op")
+    cos, sin = _check_tables(cos, sin, T, D, q_rot.device)
     dq = torch.empty_like(q_rot, memory_format=torch.contiguous_format)
     dk = torch.empty_like(k, memory_format=torch.contiguous_format)
     dv = torch.empty_like(v, memory_format=torch.contiguous_format)
@@ -330,6 +369,7 @@ def _(d_o, q_rot, k, v, o, lse, cos, sin):
 
 
 def _setup_context_rope(ctx, inputs, output):
+    _refuse_capture_with_autograd("flash_attn_bthd_rope (autograd)")
     _, k, v, cos, sin = inputs
     o, lse, q_rot = output
     ctx.save_for_backward(q_rot, k, v, o, lse, cos, sin)
@@ -337,6 +377,7 @@ def _setup_context_rope(ctx, inputs, output):
 
 
 def _backward_rope(ctx, d_o, _d_lse, _d_q_rot):
+    _refuse_capture_with_autograd("flash_attn_bthd_rope backward")
     q_rot, k, v, o, lse, cos, sin = ctx.saved_tensors
     dq, dk, dv = _flash_attn_bthd_rope_bwd(_d_out(d_o, o), q_rot, k, v, o, lse, cos, sin)
     return dq, dk, dv, None, None
@@ -348,5 +389,6 @@ _flash_attn_bthd_rope.register_autograd(_backward_rope, setup_context=_setup_con
 def flash_attn_bthd_rope(q: Tensor, k: Tensor, v: Tensor, cos: Tensor, sin: Tensor) -> Tensor:
     """Causal GQA attention in the projection layout with q's RoPE folded in: q (B, T, H, hd) *before* RoPE,
     k (B, T, KVH, hd) already rotated, v (B, T, KVH, hd), cos/sin fp32 (T_max, hd/2) -> o (B, T, H, hd)."""
+    _refuse_capture_with_autograd("flash_attn_bthd_rope", q, k, v)
     o, _, _ = _flash_attn_bthd_rope(q, k, v, cos, sin)
     return o

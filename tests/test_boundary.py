@@ -42,24 +42,6 @@ def test_abi_version():
     assert lib().nn_fa_abi_version() == ABI_VERSION
 
 
-def test_probe_library_is_separate_and_rejects_bad_arguments():
-    # bench.py --probes' measurement kernels live in their own library: the attention library exports none of
-    # them, and the probe entry points refuse arguments outside what their kernels assume (no launch then).
-    from nanonemo_amd.build import PROBE_LIB
-
-    assert PROBE_LIB.exists(), "run `python -m nanonemo_amd.build` first"
-    P = ctypes.CDLL(str(PROBE_LIB))
-    for name in ("nn_probe_coissue", "nn_probe_clock", "nn_probe_last_error"):
-        assert hasattr(P, name) and not hasattr(lib(), name), name
-    P.nn_probe_coissue.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
-    P.nn_probe_clock.argtypes = [ctypes.c_int] * 3 + [ctypes.c_void_p] * 3
-    P.nn_probe_last_error.restype = ctypes.c_char_p
-    assert P.nn_probe_coissue(8, 0, 10, 16, None) != 0 and b"invalid" in P.nn_probe_last_error()
-    assert P.nn_probe_coissue(5, 1, 10, 16, None) != 0 and b"k must be" in P.nn_probe_last_error()
-    assert P.nn_probe_clock(2, 1, 10, 16, 16, None) != 0 and b"mode must be" in P.nn_probe_last_error()
-    assert P.nn_probe_clock(0, 1, 10, None, 16, None) != 0 and b"invalid" in P.nn_probe_last_error()
-
-
 def test_timeline_build_is_separate_and_rejects_bad_arguments():
     # bench.py --timeline's library is the attention library built with NN_TIMELINE=1: it exports the same
     # attention entry points plus nn_fa_timeline_*, which the product library does not have; its record read
@@ -399,3 +381,94 @@ def test_noalloc_backward_checks_shape_before_touching_the_device():
     assert L.nn_fa_bwd_noalloc(*([None] * 9), B, H, KVH, T, D, 1, 0.125, None) == -1
     assert b"32 MiB" in L.nn_fa_last_error() or b"scratch" in L.nn_fa_last_error()
     assert L.nn_fa_bwd_noalloc(*([None] * 9), 1, 12, 5, 64, 64, 1, 0.125, None) == -1  # 12 % 5 != 0
+
+
+# ---- HIP-graph capture through autograd is refused before any launch ---------------------------
+
+
+class _Ctx:
+    """Stands in for an autograd context: the guard must raise before touching it."""
+
+    @property
+    def saved_tensors(self):
+        raise AssertionError("the guard must raise before the saved tensors are read")
+
+    def save_for_backward(self, *a):
+        raise AssertionError("the guard must raise before anything is saved")
+
+
+def test_capture_through_autograd_is_refused(monkeypatch):
+    from nanonemo_amd.kernels.hip import flash_attn as fa
+
+    monkeypatch.setattr(torch.cuda, "is_current_stream_capturing", lambda: True)
+    monkeypatch.setattr(torch.cuda, "is_available", lambda: True)
+    q = torch.zeros(1, 2, 4, 64, requires_grad=True)  # CPU tensors: the guard comes before the device check
+    k = torch.zeros(1, 1, 4, 64, requires_grad=True)
+    cos = torch.zeros(4, 32)
+    for call in (lambda: fa.flash_attn(q, k, k), lambda: fa.flash_attn_bthd(q, k, k),
+                 lambda: fa.flash_attn_bthd_rope(q, k, k, cos, cos)):
+        with pytest.raises(RuntimeError, match="not supported"):
+            call()
+    for f in (fa._setup_context, fa._setup_context_rope):
+        with pytest.raises(RuntimeError, match="capture_end"):
+            f(_Ctx(), (q, k, k, cos, cos)[: 5 if f is fa._setup_context_rope else 3], (q, q, q))
+    for f, grads in ((fa._backward, (q, None)), (fa._backward_bthd, (q, None)), (fa._backward_rope, (q, None, None))):
+        with pytest.raises(RuntimeError, match="HIP graph"):
+            f(_Ctx(), *grads)
+
+
+def test_capture_without_autograd_is_not_refused(monkeypatch):
+    # No input requires grad (or grad mode is off): nothing is recorded, so the guard lets the call through to the
+    # op's own checks (here the CPU-tensor check, since no GPU is needed to show the guard passed).
+    from nanonemo_amd.kernels.hip import flash_attn as fa
+
+    monkeypatch.setattr(torch.cuda, "is_current_stream_capturing", lambda: True)
+    monkeypatch.setattr(torch.cuda, "is_available", lambda: True)
+    q, k = torch.zeros(1, 2, 4, 64), torch.zeros(1, 1, 4, 64)
+    with pytest.raises(RuntimeError, match="CUDA tensors"):
+        fa.flash_attn(q, k, k)
+    qg = q.clone().requires_grad_()
+    with torch.no_grad(), pytest.raises(RuntimeError, match="CUDA tensors"):
+        fa.flash_attn(qg, k, k)
+
+
+def test_capture_guard_is_off_when_not_capturing():
+    from nanonemo_amd.kernels.hip import flash_attn as fa
+
+    q = torch.zeros(1, 2, 4, 64, requires_grad=True)
+    fa._refuse_capture_with_autograd("x", q)  # not capturing: returns
+
+
+def test_rope_fused_ops_reject_host_tables():
+    # cos / sin must be GPU tensors on q's device; a host table would reach the library as a host address.
+    from nanonemo_amd.kernels.hip import flash_attn as fa
+
+    cos = torch.zeros(8, 32)
+    with pytest.raises(RuntimeError, match="inputs' device"):
+        fa._check_tables(cos, cos, 8, 64, torch.device("cuda", 0))
+    with pytest.raises(RuntimeError, match="inputs' device"):
+        fa._check_tables(cos, cos.clone(), 8, 64, torch.device("cpu"))  # CPU "inputs" still need CUDA tables
+
+
+def test_backward_ops_refuse_capture_only_inside_the_autograd_engine(monkeypatch):
+    # The backward ops' own guard: a capture driven by the autograd engine (eager autograd, or a compiled backward
+    # as mode="reduce-overhead" records) is refused; the same call outside the engine is not (a manual op pair).
+    from nanonemo_amd.kernels.hip import flash_attn as fa
+
+    monkeypatch.setattr(torch.cuda, "is_current_stream_capturing", lambda: True)
+    monkeypatch.setattr(torch.cuda, "is_available", lambda: True)
+    fa._refuse_capture_from_autograd_engine("outside the engine")  # returns
+
+    class F(torch.autograd.Function):
+        @staticmethod
+        def forward(ctx, a):
+            return a * 2
+
+        @staticmethod
+        def backward(ctx, g):
+            fa._refuse_capture_from_autograd_engine("inside the engine")
+            return g
+
+    x = torch.ones(3, requires_grad=True)
+    with pytest.raises(RuntimeError, match="inside the engine: capturing"):
+        F.apply(x).sum().backward()
