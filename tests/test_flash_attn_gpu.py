@@ -51,7 +51,70 @@ def _run(q, k, v, do):
     return o.detach().cpu(), lse.cpu(), q.grad.cpu(), k.grad.cpu(), v.grad.cpu()
 
 
-def _check(got, ref, dtype, label):
+# Criterion (i) of the tolerance proposal: the kernel's error against the reference, next to PyTorch's own attention
+# in the same dtype on the same rounded inputs, measured in the same run, on max-abs and relative-Frobenius error:
+#   * at most SDPA_RATIO times the error of PyTorch's FlashAttention kernel (SDPA's flash backend, else its
+#     mem-efficient one): the same algorithm class, which like this kernel (and the reference's,
+#     /root/reference/nanonemo/kernels/cuda/flash_attn.cu:129-138,287-293) rounds P and dS to 16 bits before their
+#     products and builds D from the 16-bit o;
+#   * at most SDPA_MATH_RATIO times the error of SDPA's math backend, which computes in fp32 and rounds only its
+#     outputs. dq is where the two differ: dq = scale * sum_j dS_ij K_j with sum_j dS_ij = 0, so the 16-bit rounding
+#     of dS shows through the cancellation (measured up to 2.7x max-abs and 3.3x relative-Frobenius at inputs x3, the
+#     same ratios PyTorch's own flash kernel shows against the math path).
+# SDPA_FLOOR absorbs max-abs errors at the level of fp32 rounding noise (dq at T = 1, which both SDPA paths return as
+# exact zeros); the relative-Frobenius ratio is not taken for an all-zero reference.
+SDPA_RATIO = 2.0
+SDPA_MATH_RATIO = 4.0
+SDPA_FLOOR = 1e-5
+
+
+def _sdpa(q, k, v, do, backends):
+    """PyTorch's attention in the inputs' dtype on the GPU: repeat_interleave'd K/V through SDPA restricted to the
+    first of ``backends`` that runs, with autograd; returns (backend name, (o, dq, dk, dv) on the CPU)."""
+    from torch.nn.attention import sdpa_kernel
+
+    group = q.shape[1] // k.shape[1]
+    for backend in backends:
+        qs, ks, vs = (t.to(DEV).requires_grad_() for t in (q, k, v))
+        try:
+            with sdpa_kernel(backend):
+                o = torch.nn.functional.scaled_dot_product_attention(
+                    qs, ks.repeat_interleave(group, dim=1), vs.repeat_interleave(group, dim=1), is_causal=True)
+        except RuntimeError:  # the backend does not take this shape or dtype
+            continue
+        grads = torch.autograd.grad(o, (qs, ks, vs), do.to(DEV))
+        torch.cuda.synchronize()
+        return backend.name, tuple(t.detach().cpu() for t in (o, *grads))
+    raise RuntimeError(f"no SDPA backend of {backends} ran")
+
+
+def _sdpa_bound(report, refs, inputs, label):
+    """Assert criterion (i) (see SDPA_RATIO) for o, dq, dk, dv and print the ratios."""
+    from torch.nn.attention import SDPBackend
+
+    lines = []
+    for backends, ratio in (((SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION), SDPA_RATIO),
+                            ((SDPBackend.MATH,), SDPA_MATH_RATIO)):
+        name, outs = _sdpa(*inputs, backends)
+        parts = []
+        for n, x in zip(("o", "dq", "dk", "dv"), outs):
+            r = refs[n]
+            es = errors(x, r)
+            ours = report[n]
+            metrics = ("max_abs", "rel_fro") if bool((r != 0).any()) else ("max_abs",)
+            for m in metrics:
+                floor = SDPA_FLOOR if m == "max_abs" else 0.0
+                assert ours[m] <= ratio * es[m] + floor, (
+                    f"{label} {n}: {m} {ours[m]:.3e} is more than {ratio} x SDPA {name}'s {es[m]:.3e}")
+            parts.append(f"{n} {ours['max_abs'] / max(es['max_abs'], SDPA_FLOOR):.2f}x/"
+                         f"{ours['rel_fro'] / max(es['rel_fro'], 1e-12):.2f}x")
+        lines.append(f"vs {name} (bound {ratio}x): " + ", ".join(parts))
+    print(f"[sdpa] {label} (max-abs/rel-fro ratios) " + "; ".join(lines), flush=True)
+
+
+def _check(got, ref, dtype, label, inputs=None):
+    """Tolerances of tests/common.py against ``ref``; with ``inputs`` (the rounded q, k, v, dO) also criterion (i):
+    o, dq, dk, dv against PyTorch's same-dtype attention (SDPA_RATIO)."""
     o, lse, dq, dk, dv = got
     ro, rlse, rdq, rdk, rdv = ref
     assert o.dtype == dtype and dq.dtype == dtype and dk.dtype == dtype and dv.dtype == dtype
@@ -62,6 +125,8 @@ def _check(got, ref, dtype, label):
     for name, x, r in (("dq", dq, rdq), ("dk", dk, rdk), ("dv", dv, rdv)):
         report[name] = assert_close_tol(x, r, TOL_GRAD[dtype], f"{label} {name}")
     print(f"\n[parity] {label}: " + ", ".join(f"{k} max_abs={v['max_abs']:.2e} fro={v['rel_fro']:.1e}" for k, v in report.items()), flush=True)
+    if inputs is not None:
+        _sdpa_bound(report, {"o": ro, "dq": rdq, "dk": rdk, "dv": rdv}, inputs, label)
 
 
 def _oracle(q, k, v, do):
@@ -75,14 +140,15 @@ def _oracle(q, k, v, do):
 def test_golden_fixture(name):
     g = load_golden(name)
     got = _run(g["q"], g["k"], g["v"], g["do"])
-    _check(got, tuple(g[x] for x in ("o", "lse", "dq", "dk", "dv")), g["dtype"], f"golden {name}")
+    _check(got, tuple(g[x] for x in ("o", "lse", "dq", "dk", "dv")), g["dtype"], f"golden {name}",
+           inputs=(g["q"], g["k"], g["v"], g["do"]))
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("B, H, KVH, T, hd", REF_SHAPES)
 def test_matches_oracle(B, H, KVH, T, hd, dtype):
     q, k, v, do = make_inputs(B, H, KVH, T, hd, dtype, seed=0)
-    _check(_run(q, k, v, do), _oracle(q, k, v, do), dtype, f"{(B, H, KVH, T, hd)} {dtype}")
+    _check(_run(q, k, v, do), _oracle(q, k, v, do), dtype, f"{(B, H, KVH, T, hd)} {dtype}", inputs=(q, k, v, do))
 
 
 # Ragged lengths around every tile size (64-key forward tiles, 128-query forward blocks, 64-query /
@@ -359,7 +425,8 @@ def test_compiles_with_strided_inputs():
 
 @pytest.mark.skip(
     reason="capturing fwd+bwd (with autograd) in torch.cuda.graph ended in a host segmentation fault inside "
-    "capture_end on the MI355X box; no cause has been shown in this code yet, so the case stays off the GPU"
+    "capture_end on the MI355X box; no cause has been shown in this code yet, so the case stays off the GPU and the "
+    "ops refuse it before any launch (tests/test_boundary.py::test_capture_through_autograd_is_refused)"
 )
 def test_hip_graph_capture_and_replay():
     # fwd+bwd captured once, replayed several times with eager work in between; every replay must
@@ -431,6 +498,7 @@ def test_baseline_configs_full_size(B, H, KVH, T, hd, dtype, mult):
     dq, dk, dv = torch.autograd.grad(o, (qs, ks, vs), do)
     got = (o.detach(), lse, dq, dk, dv)
     ref = _torch_fp32_reference(q, k, v, do)
-    _check(tuple(t.cpu() for t in got), tuple(t.cpu() for t in ref), dtype, f"config {(B, H, KVH, T, hd, dtype, mult)}")
+    _check(tuple(t.cpu() for t in got), tuple(t.cpu() for t in ref), dtype, f"config {(B, H, KVH, T, hd, dtype, mult)}",
+           inputs=(q, k, v, do))
     del ref
     torch.cuda.empty_cache()

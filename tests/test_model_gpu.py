@@ -19,12 +19,14 @@ SMALL = dict(n_layers=2, d_model=256, n_heads=4, n_kv_heads=2, d_ff=512, vocab_s
 
 
 def _pair(attn: str, cfg: dict = SMALL, batch: int = 2):
-    """The plain model and one with this build's kernels ("+rope" / "+norm": also the HIP RoPE / fused add +
-    RMSNorm), on identical weights, with a batch of uniform token ids and their next-token targets."""
+    """The plain model and one with this build's kernels ("+rope" / "+qrope" / "+norm": also the HIP RoPE, q's RoPE
+    inside the attention op, the fused add + RMSNorm), on identical weights, with a batch of uniform token ids and
+    their next-token targets."""
     kernel, *extras = attn.split("+")
     torch.manual_seed(0)
     ref = NanoNemo(ModelConfig(**cfg)).cuda()
-    fast = NanoNemo(ModelConfig(**cfg, attn_kernel=kernel, rope_kernel="hip" if "rope" in extras else "torch",
+    rope = "hip" if "rope" in extras else "fused" if "qrope" in extras else "torch"
+    fast = NanoNemo(ModelConfig(**cfg, attn_kernel=kernel, rope_kernel=rope,
                                 norm_kernel="hip" if "norm" in extras else "torch")).cuda()
     fast.load_state_dict(ref.state_dict())
     idx = torch.randint(0, ref.cfg.vocab_size, (batch, ref.cfg.max_seq_len), device="cuda")
@@ -56,7 +58,7 @@ def test_bf16_autocast_loss_and_grads_match_torch_attention(attn):
 CONFIG5 = dict(max_seq_len=1024, attn_backend="math_fp32")
 
 
-@pytest.mark.parametrize("attn", ["hip_bthd", "hip", "hip_bthd+rope+norm"])
+@pytest.mark.parametrize("attn", ["hip_bthd", "hip", "hip_bthd+rope+norm", "hip_bthd+qrope+norm"])
 def test_config5_full_size_loss_and_grads_match_torch_attention(attn):
     # The pattern of /root/reference/tests/kernels/test_model_kernels.py:54-66 (loss 1e-3, every gradient within
     # 5e-2 of its largest magnitude) at the full model and batch, widened for bf16: loss 5e-3.
@@ -105,6 +107,29 @@ def test_compiled_model_has_no_graph_breaks():
         _, eager_loss = fast(idx, tgt)
     loss.backward()
     torch.testing.assert_close(loss, eager_loss, rtol=1e-3, atol=1e-3)
+
+
+@pytest.mark.parametrize("attn", ["hip_bthd+rope+norm", "hip_bthd+qrope+norm"])
+def test_compiled_model_with_every_hip_kernel(attn):
+    # The whole model compiled with every kernel of this build on (the pattern of
+    # /root/reference/tests/kernels/test_model_kernels.py:69-78): no graph break under fullgraph=True, and the
+    # compiled forward and backward agree with the same model run eagerly.
+    print(f"\n[case] torch.compile(fullgraph=True) of the model with {attn}", flush=True)
+    _, fast, idx, tgt = _pair(attn)
+    torch.manual_seed(0)
+    eager = NanoNemo(fast.cfg).cuda()
+    eager.load_state_dict(fast.state_dict())
+    torch._dynamo.reset()
+    compiled = torch.compile(fast, fullgraph=True)
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        _, loss = compiled(idx, tgt)
+        _, eager_loss = eager(idx, tgt)
+    loss.backward()
+    eager_loss.backward()
+    torch.testing.assert_close(loss, eager_loss, rtol=1e-3, atol=1e-3)
+    for (name, g), r in zip(_grads(fast).items(), _grads(eager).values()):
+        assert g is not None and torch.isfinite(g).all(), name
+        torch.testing.assert_close(g, r, rtol=5e-2, atol=5e-2 * r.abs().max().item(), msg=name)
 
 
 def test_short_training_run_tracks_torch_attention():

@@ -105,3 +105,12 @@ def test_fused_rope_compiles_without_graph_breaks():
     fn = torch.compile(lambda q, k, v: fa.flash_attn_bthd_rope(q, rp.rope_k(k, cos, sin), v, cos, sin), fullgraph=True)
     eager = fa.flash_attn_bthd_rope(q, rp.rope_k(k, cos, sin), v, cos, sin)
     assert torch.equal(fn(q, k, v), eager)
+    # the backward under AOTAutograd: the three-output op with its ignored gradients (lse, q_rot) and the
+    # rope_k backward, bit for bit against eager autograd
+    outs = []
+    for f in (fn, lambda q, k, v: fa.flash_attn_bthd_rope(q, rp.rope_k(k, cos, sin), v, cos, sin)):
+        qs, ks, vs = (t.clone().requires_grad_() for t in (q, k, v))
+        o = f(qs, ks, vs)
+        outs.append((o.detach(), *torch.autograd.grad(o, (qs, ks, vs), do)))
+    for name, a, b in zip(("o", "dq", "dk", "dv"), *outs):
+        assert torch.equal(a, b), name
