@@ -2,7 +2,6 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--dtype bf16|fp16] [--batch 8] [--seq 1024]
     python bench.py --sweep        # step and per-kernel times over the SWEEP shapes, one JSON line each
-    python bench.py --probes       # VALU/MFMA co-issue table and shader clock under load (probe library)
     python bench.py --timeline     # per-block timelines of the three attention kernels (timeline build)
 
 A step is one forward + backward of the hot path through the drop-in torch.library ops (nanonemo::flash_attn
@@ -24,8 +23,10 @@ The JSON line also carries:
   roofline      the dominant kernel (the longest of the forward, dK/dV and dQ kernels), timed alone
                 with HIP events on the stream it is launched on: achieved = its algorithmic FLOPs per
                 launch (forward 4*D, dK/dV 6*D, dQ 2*D per causal pair) / its mean launch time, against
-                the dense BF16/FP16 MFMA peak of 2.5 PFLOP/s; traffic = its HBM bytes per launch from the
-                committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary of this workload;
+                the dense BF16/FP16 MFMA peak of 2.5 PFLOP/s; traffic is null (HBM bytes need rocprofv3
+                counters, which this run does not collect);
+  traffic_committed  the dominant kernel's HBM bytes per launch from the committed rocprofv3 FETCH_SIZE /
+                WRITE_SIZE summary of this workload (profiles/), labelled as such;
   clock         the GFX clock (median of the SMU's per-XCD readings through amdsmi) and socket power while
                 the dK/dV kernel alone, then the whole step, run back to back; roofline.frac_at_sclk is the
                 dominant kernel's fraction of the peak scaled to that clock (the published peak assumes 2.4 GHz);
@@ -41,6 +42,9 @@ The JSON line also carries:
                 nanonemo::flash_attn_bthd ops, with the host's time per step beside each;
   rope_qk       the HIP RoPE kernel on the workload's q and k (projection layout, one launch) and its
                 HBM rate, beside the plain-PyTorch formula;
+  config5       BASELINE config 5 in brief (default workload only): a few 114 M-model bf16 train steps per
+                attention path (plain PyTorch, and every HIP kernel with q's RoPE separate or folded in):
+                tokens/s and the loss differences against the plain-PyTorch path (step 0 and largest);
   add_rmsnorm   the HIP fused residual add + RMSNorm forward and backward (dx, ddelta and dw) on the
                 114 M model's stream at this workload's tokens (B*T rows of 768, fp32 residual, bf16
                 sublayer output and normalised output) and their HBM rates.
@@ -260,13 +264,12 @@ def parse():
     p.add_argument("--input-scale", type=float, default=1.0, help="q, k, v ~ N(0,1) times this (BASELINE config 3: 3.0)")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=16.0, help="budget of the CPU baseline sample (both forms)")
+    p.add_argument("--no-config5", action="store_true", help="skip the config5 block (114 M model train steps)")
+    p.add_argument("--config5-steps", type=int, default=10, help="train steps per attention path in the config5 block")
     p.add_argument("--profile-only", action="store_true", help="only the timed steps (for rocprofv3)")
     p.add_argument("--prewarm", type=float, default=1.0, help="seconds of untimed steps after the warmup")
     p.add_argument("--sweep", action="store_true",
                    help="instead of the headline line: one JSON line per shape of SWEEP (step and per-kernel times)")
-    p.add_argument("--probes", action="store_true",
-                   help="instead of the headline line: the VALU/MFMA co-issue table and the shader clock under load "
-                   "(nanonemo_amd/csrc/probe.hip), one JSON line")
     p.add_argument("--timeline", action="store_true",
                    help="instead of the headline line: per-block timelines of the forward, dQ and dK/dV kernels at "
                    "the workload's shape, from libnanonemo_fa_timeline.so, one JSON line")
@@ -377,6 +380,34 @@ def sweep(args):
         torch.cuda.empty_cache()
 
 
+def config5(steps: int, warmup: int = 4):
+    """BASELINE config 5 in brief: the 114 M model (12 layers, d_model 768, 12 Q / 4 KV heads, vocab 50,304, tied
+    embeddings) trained from the seed-0 init on the seed-0 uniform token stream at B=8, T=1024 under bf16 autocast,
+    ``steps`` AdamW steps per attention path (nanonemo_amd.train.run, the same weights and batches for every path).
+    tokens/s over the steps after ``warmup``; loss differences against the plain-PyTorch attention (SDPA math on fp32
+    q, k, v), at step 0 (identical weights and batch) and the largest over the steps. The 50-step curves come from
+    ``python -m nanonemo_amd.train``."""
+    import torch
+
+    from nanonemo_amd.train import run
+
+    paths = ("torch", "hip_bthd+rope+norm", "hip_bthd+qrope+norm")
+    res = {}
+    for attn in paths:
+        losses, tps, fpt = run(attn, steps, 8, 1024, dict(max_seq_len=1024, attn_backend="math_fp32"), warmup=warmup)
+        res[attn] = {"tokens_per_s": round(tps, 1), "model_tflops": round(tps * fpt / 1e12, 2),
+                     "losses": [round(v, 5) for v in losses]}
+        torch.cuda.empty_cache()
+    for attn in paths[1:]:
+        d = [abs(a - b) for a, b in zip(res[attn]["losses"], res["torch"]["losses"])]
+        res[attn]["step0_abs_loss_diff_vs_torch"] = round(d[0], 6)
+        res[attn]["max_abs_loss_diff_vs_torch"] = round(max(d), 5)
+        res[attn]["speedup_vs_torch"] = round(res[attn]["tokens_per_s"] / res["torch"]["tokens_per_s"], 3)
+    return {"workload": f"114M NanoNemo, bf16 autocast, B=8 T=1024, {steps} AdamW steps per path (tokens/s over the "
+                        f"last {steps - warmup}), seed-0 init, uniform synthetic tokens; torch = SDPA math on fp32 q, k, v",
+            "results": res}
+
+
 def _cpu_topology():
     """(usable logical CPUs, physical cores among them, CPU model) of this host, from the process's CPU
     affinity and /proc/cpuinfo (a core is a distinct (physical id, core id) pair)."""
@@ -453,72 +484,6 @@ def cpu_baseline(budget_s):
         "physical_cores": phys,
         "cpu_model": model,
     }
-
-
-def probes():
-    """The measurements the kernels' design rests on, from the probe library (nanonemo_amd/csrc/probe.hip):
-    - coissue: time per 32x32x16 bf16 MFMA per SIMD when every MFMA is followed by K independent fp32 FMAs, with
-      1-4 waves resident per SIMD (as cycles at 2.4 GHz, converted from the measured rate);
-    - clock: the shader clock from per-wave s_memtime / s_memrealtime stamps around back-to-back MFMAs (1 and 4
-      waves per SIMD) and FMAs only (4 waves per SIMD), and the shader cycles per MFMA with one wave per SIMD."""
-    import torch
-
-    from nanonemo_amd.build import PROBE_LIB
-
-    if not PROBE_LIB.exists():
-        raise RuntimeError(f"{PROBE_LIB} is not built; run `python -m nanonemo_amd.build`")
-    P = ctypes.CDLL(str(PROBE_LIB))
-    P.nn_probe_coissue.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
-    P.nn_probe_clock.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p,
-                                 ctypes.c_void_p]
-    P.nn_probe_last_error.restype = ctypes.c_char_p
-
-    def ok(rc):
-        if rc != 0:
-            raise RuntimeError(P.nn_probe_last_error().decode())
-
-    dev = torch.device("cuda:0")
-    ncu = torch.cuda.get_device_properties(dev).multi_processor_count
-    sp = torch.cuda.current_stream().cuda_stream
-    n = 4000
-    sink = torch.empty(4 * ncu * 256, device=dev)
-    coissue = {}
-    for wps in (1, 2, 3, 4):
-        blocks = ncu * wps  # 4 waves per block: one per SIMD of its CU
-        row = {}
-        for k in (0, 4, 8, 12, 16):
-            for _ in range(2):
-                ok(P.nn_probe_coissue(k, blocks, n, sink.data_ptr(), sp))
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            e0.record()
-            ok(P.nn_probe_coissue(k, blocks, n, sink.data_ptr(), sp))
-            e1.record()
-            e1.synchronize()
-            s = e0.elapsed_time(e1) * 1e-3
-            mfma_per_simd = wps * 4 * n
-            row[f"K={k}"] = round(s / mfma_per_simd * 2.4e9, 1)
-        coissue[f"{wps} waves/SIMD"] = row
-    clock = {}
-    for label, mode, wps in (("mfma, 1 wave/SIMD", 0, 1), ("mfma, 4 waves/SIMD", 0, 4), ("fma, 4 waves/SIMD", 1, 4)):
-        blocks = ncu * wps
-        stamps = torch.zeros(blocks * 16, dtype=torch.int64, device=dev)
-        for _ in range(3):
-            ok(P.nn_probe_clock(mode, blocks, 20000, stamps.data_ptr(), sink.data_ptr(), sp))
-        torch.cuda.synchronize()
-        st = stamps.view(-1, 4).cpu().double()
-        mhz = ((st[:, 1] - st[:, 0]) / ((st[:, 3] - st[:, 2]) / 100.0)).sort().values
-        entry = {"mhz_median": round(mhz[len(mhz) // 2].item()), "mhz_min": round(mhz[0].item()),
-                 "mhz_max": round(mhz[-1].item())}
-        if mode == 0 and wps == 1:  # (with several waves a wave's lifetime is not the SIMD's busy time)
-            entry["shader_cycles_per_mfma_per_wave"] = round(((st[:, 1] - st[:, 0]).median() / (4 * 20000)).item(), 1)
-        clock[label] = entry
-    print(json.dumps({"probes": {
-        "coissue_cycles_per_mfma_per_simd_at_2400mhz": coissue,
-        "coissue_how": "each wave: 32x32x16 bf16 MFMAs on 4 accumulators, each followed by K independent fp32 FMAs; "
-                       "time per MFMA per SIMD from HIP events, as cycles at 2.4 GHz (a lone MFMA is 32 shader cycles)",
-        "clock": clock,
-        "cus": ncu,
-    }}), flush=True)
 
 
 def timeline(args):
@@ -654,9 +619,6 @@ def main():
         return
     if args.sweep and args.gpus == 1:
         sweep(args)
-        return
-    if args.probes and args.gpus == 1:
-        probes()
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(
@@ -1005,14 +967,18 @@ def main():
     dominant = max(("fwd", "bwd_dkdv", "bwd_dq"), key=lambda n: kern_us[n])
     kernel_names = {"fwd": "fa_fwd_kernel", "bwd_dkdv": "fa_bwd_dkdv_kernel", "bwd_dq": "fa_bwd_dq_kernel"}
 
-    # HBM bytes per launch of the dominant kernel, from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE
-    # summary of this workload (profiles/), when one exists for it.
-    traffic = None
+    # HBM bytes per launch of the dominant kernel are not measured in this run (that needs rocprofv3 counters): the
+    # committed FETCH_SIZE / WRITE_SIZE summary of this workload (profiles/) is reported beside the roofline block,
+    # labelled with its source, and roofline.traffic stays null.
+    traffic_committed = None
     tfile = ROOT / "profiles" / f"fa_causal_gqa_b{B}_t{T}_{args.dtype}.traffic.json"
     if tfile.exists() and (H, KVH, D) == (12, 4, 64):
         measured = json.loads(tfile.read_text())
         key = f"{kernel_names[dominant]}<{D},{args.dtype}>"
-        traffic = round(measured[key]) if key in measured else None
+        if key in measured:
+            traffic_committed = {"kernel": kernel_names[dominant], "bytes_per_launch": round(measured[key]),
+                                 "source": f"profiles/{tfile.name}: rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE of this "
+                                 "workload, scaled by a device copy's readings; committed, not measured in this run"}
 
     value = f_all / (ms * 1e-3) / 1e12
     props = torch.cuda.get_device_properties(dev)
@@ -1106,12 +1072,13 @@ def main():
             "peak": PEAK_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(kern_tflops[dominant] / PEAK_TFLOPS, 4),
-            "traffic": traffic,
+            "traffic": None,
             # the same peak scaled to the GFX clock measured while the kernel ran back to back
             "sclk_mhz": sclk,
             "peak_at_sclk": round(PEAK_TFLOPS * sclk / 2400.0, 1) if sclk else None,
             "frac_at_sclk": round(kern_tflops[dominant] / (PEAK_TFLOPS * sclk / 2400.0), 4) if sclk else None,
         },
+        "traffic_committed": traffic_committed,
         "clock": clocks,
         "kernels": {
             "fwd_us": round(kern_us["fwd"], 2),
@@ -1128,6 +1095,10 @@ def main():
         },
         "device": {"name": props.name, "cus": props.multi_processor_count, "arch": getattr(props, "gcnArchName", "")},
     }
+    if not args.no_config5 and (B, T, H, KVH, D) == (8, 1024, 12, 4, 64):
+        del graph, flush
+        torch.cuda.empty_cache()
+        out["config5"] = config5(args.config5_steps)
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
     print(json.dumps(out), flush=True)
