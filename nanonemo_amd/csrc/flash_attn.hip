@@ -749,11 +749,15 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(
             }
         }
     };
-    // Iteration itn of the unit whose query tiles start at tile qtf: query head iter_head of the group,
-    // query tile iter_tile. With several waves per pair head-minor, so that the group's diagonal
-    // iterations, which carry the mask, go to different waves; with one wave head-major.
-    auto iter_head = [&](int itn, int qtf) { return WPP > 1 ? itn % group : itn / (nqt - qtf); };
-    auto iter_tile = [&](int itn, int qtf) { return qtf + (WPP > 1 ? itn / group : itn % (nqt - qtf)); };
+    // Iteration itn of unit qtf (whose query tiles run from qtf to nqt - 1): query head iter_head of the group,
+    // query tile iter_tile. Head-minor, so that the group's diagonal iterations, which carry the mask, go to
+    // different waves. The pair's first unit (pj, the longer) walks its tiles down from the last one, the second
+    // (nkb - 1 - pj) up from its own: at the pair's i-th iteration every pair of the (batch, KV head) is then on
+    // tile nqt - 1 - i / group in its first unit or on tile i / group - 1 in its second, whichever pair it is. The
+    // pairs' blocks of one (batch, KV head) run on one XCD and start together, so they ask for the same Q / dO
+    // tiles at about the same time and share them in that XCD's L2 (at most two tiles per head in flight).
+    auto iter_head = [&](int itn, int qtf) { (void)qtf; return itn % group; };
+    auto iter_tile = [&](int itn, int qtf) { return qtf == pj ? nqt - 1 - itn / group : qtf + itn / group; };
     // DMA iteration itn into this wave's slot: the Q / dO tiles and the -lse/scale, -D vectors.
     auto issue_it = [&](int itn, int qtf, u16* qs, u16* os, float* ls) {
         // Wave-uniform in fact; made uniform for the compiler only here, so that the tile addressing is

@@ -81,6 +81,31 @@ def emulate_split(B, H, KVH, T, D):
 SHAPES = [(2, 12, 1, 1024, 64), (8, 12, 1, 1024, 64), (1, 12, 4, 1024, 64), (1, 12, 4, 400, 32), (2, 6, 2, 333, 64)]
 
 
+def iteration(itn, unit, first_unit, group, nqt):
+    """Restates the dK/dV kernel's iter_head / iter_tile: iteration itn of unit ``unit`` of a pair whose first unit
+    is ``first_unit`` -> (query head of the group, query tile), head-minor; the first unit's tiles descend from the
+    last, the second unit's ascend from its own."""
+    t = nqt - 1 - itn // group if unit == first_unit else unit + itn // group
+    return itn % group, t
+
+
+@pytest.mark.parametrize("group, nqt", [(3, 16), (1, 16), (12, 16), (3, 128), (4, 7), (2, 1), (3, 15)])
+def test_pairs_cover_their_iterations_once_and_walk_the_tiles_in_step(group, nqt):
+    nkb = nqt
+    for pj in range((nkb + 1) // 2):
+        units = [pj] if nkb - 1 - pj == pj else [pj, nkb - 1 - pj]
+        walk = []
+        for unit in units:
+            n = group * (nqt - unit)
+            got = [iteration(i, unit, pj, group, nqt) for i in range(n)]
+            assert sorted(got) == sorted((h, t) for h in range(group) for t in range(unit, nqt))
+            walk += got
+        # at the pair's i-th iteration every pair of the (batch, KV head) is on tile nqt - 1 - i // group (first
+        # unit) or i // group - 1 (second unit), whichever pair it is
+        for i, (h, t) in enumerate(walk):
+            assert h == i % group and t == (nqt - 1 - i // group if i < group * (nqt - pj) else i // group - 1)
+
+
 @pytest.mark.parametrize("shape", SHAPES)
 def test_split_partials_are_each_stored_once_and_every_iteration_is_taken_once(shape):
     B, H, KVH, T, D = shape
@@ -107,3 +132,42 @@ def test_the_replay_shape_splits_sixteen_ways():
     S, regions, total = carve(2, 12, 1, 1024, 64)
     assert S == 16 and set(regions) == {"nD", "nL", "part"}
     assert regions["part"][1] - regions["part"][0] == 16 * 2 * 4 * 2 * 1 * 1024 * 64
+
+
+# ---- forward / dQ grid: block -> (batch * H + head, query block) ---------------------------------
+
+
+def qblock_of(bid, BH, group, nqb):
+    """Restates qblock_of() of nanonemo_amd/csrc/flash_attn.hip: heaviest query blocks first; when the B*KVH head
+    groups divide evenly over the 8 XCDs, every query head of group g goes to XCD g % 8 (block i runs on XCD i % 8)."""
+    G = BH // group
+    if G % 8 == 0:
+        x, slot = bid & 7, bid >> 3
+        per = (G >> 3) * group
+        qi, r = divmod(slot, per)
+        gi, hq = divmod(r, group)
+        return (gi * 8 + x) * group + hq, nqb - 1 - qi
+    return bid % BH, nqb - 1 - bid // BH
+
+
+@pytest.mark.parametrize(
+    "B, H, KVH, T",
+    [(8, 12, 4, 1024), (32, 12, 4, 1024), (2, 12, 4, 8192), (1, 12, 4, 256), (8, 12, 12, 1024), (8, 12, 1, 1024),
+     (3, 8, 2, 65), (2, 4, 4, 37), (16, 16, 8, 512), (4, 6, 2, 300), (1, 1, 1, 1), (5, 12, 3, 130)],
+)
+def test_qblock_of_covers_every_block_once_heaviest_first_per_xcd(B, H, KVH, T):
+    BH, group, nqb = B * H, H // KVH, (T + 127) // 128
+    seen = {}
+    for bid in range(nqb * BH):
+        bh, qb = qblock_of(bid, BH, group, nqb)
+        assert 0 <= bh < BH and 0 <= qb < nqb
+        assert (bh, qb) not in seen, f"block {bid} repeats {(bh, qb)} of block {seen[(bh, qb)]}"
+        seen[(bh, qb)] = bid
+    assert len(seen) == nqb * BH
+    # Dispatch order within each XCD (block i on XCD i % 8): the causal work (qb + 1 key tiles) never grows.
+    for x in range(8):
+        qbs = [qblock_of(bid, BH, group, nqb)[1] for bid in range(x, nqb * BH, 8)]
+        assert all(a >= b for a, b in zip(qbs, qbs[1:])), f"XCD {x}: query blocks {qbs[:12]}..."
+    if (BH // group) % 8 == 0:  # every query head of one (batch, KV head) group shares one XCD
+        for (bh, _), bid in seen.items():
+            assert (bh // group) % 8 == bid % 8
