@@ -42,6 +42,8 @@ The JSON line also carries:
                 nanonemo::flash_attn_bthd ops, with the host's time per step beside each;
   rope_qk       the HIP RoPE kernel on the workload's q and k (projection layout, one launch) and its
                 HBM rate, beside the plain-PyTorch formula;
+  other_dtype   the headline's measurement in the other 16-bit type (fp16 for the default bf16 run: BASELINE
+                config 2's own dtype);
   config5       BASELINE config 5 in brief (default workload only): a few 114 M-model bf16 train steps per
                 attention path (plain PyTorch, and every HIP kernel with q's RoPE separate or folded in):
                 tokens/s and the loss differences against the plain-PyTorch path (step 0 and largest);
@@ -952,6 +954,33 @@ def main():
     # allocation, which would slow the measurements after it)
     sdpa_cmp = same_node(q, k, v, do, fa, max(20, args.steps // 2))
 
+    # BASELINE config 2's own dtype: the same op pair on the same seeded inputs in the other 16-bit type, timed as the
+    # headline (warm-up, settling steps, then K steps each after a cache flush, median).
+    other = torch.float16 if dtype == torch.bfloat16 else torch.bfloat16
+    q2, k2, v2, do2 = (t.to(other) for t in (q, k, v, do))
+
+    def step_op2():
+        o3, lse3 = fa._flash_attn(q2, k2, v2)
+        return fa._flash_attn_bwd(do2, q2, k2, v2, o3, lse3)
+
+    for _ in range(args.warmup):
+        step_op2()
+    t_end = time.perf_counter() + args.prewarm / 2
+    while time.perf_counter() < t_end:
+        for _ in range(100):
+            step_op2()
+        torch.cuda.synchronize()
+    ev2 = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    for i, (a, b_) in enumerate(ev2):
+        flush.fill_(i & 0xFF)
+        a.record(stream)
+        step_op2()
+        b_.record(stream)
+    torch.cuda.synchronize()
+    other_ms = statistics.median(a.elapsed_time(b_) for a, b_ in ev2)
+    del q2, k2, v2, do2
+
     e = 2  # bytes per 16-bit element
     pre_alg_bytes = 2 * B * H * T * D * e + 4 * B * H * T
     pre_all_bytes = pre_alg_bytes + 8 * B * H * T  # also reads lse and writes -lse/scale
@@ -1010,6 +1039,12 @@ def main():
             "mean": round(statistics.fmean(step_ms), 5),
         },
         # warm caches, back to back (the inputs stay in the 256 MB Infinity Cache between steps)
+        "other_dtype": {
+            "dtype": "fp16" if other == torch.float16 else "bf16",
+            "how": "the same op pair on the same seeded inputs cast to the other 16-bit type, timed as the headline",
+            "ms_per_step": round(other_ms, 5),
+            "value": round(f_all / (other_ms * 1e-3) / 1e12, 2),
+        },
         "c_abi_warm_ms_per_step": round(abi_ms, 5),
         "c_abi_warm_tflops": round(f_all / (abi_ms * 1e-3) / 1e12, 2),
         "op_warm_ms_per_step": round(op_ms, 5),
