@@ -76,9 +76,13 @@ def _refuse_capture_with_autograd(where: str, *inputs: Tensor) -> None:
     public functions (grad mode on and an input requires grad), and in setup_context / the backward as a
     backstop for direct op calls. Capture without autograd, and capture of the C ABI, are unaffected. Skipped
     while torch.compile traces (the check is a host query, and no capture runs at trace time)."""
+    # A capture needs PyTorch's initialised HIP state: is_initialized is a flag read, where the capture query is a
+    # runtime call, and this runs on every op call.
+    if not torch.cuda.is_initialized():
+        return
     if inputs and not (torch.is_grad_enabled() and any(t.requires_grad for t in inputs)):
         return
-    if torch.compiler.is_compiling() or not (torch.cuda.is_available() and torch.cuda.is_current_stream_capturing()):
+    if torch.compiler.is_compiling() or not torch.cuda.is_current_stream_capturing():
         return
     raise RuntimeError(_CAPTURE_MSG.format(where))
 

@@ -401,7 +401,7 @@ def test_capture_through_autograd_is_refused(monkeypatch):
     from nanonemo_amd.kernels.hip import flash_attn as fa
 
     monkeypatch.setattr(torch.cuda, "is_current_stream_capturing", lambda: True)
-    monkeypatch.setattr(torch.cuda, "is_available", lambda: True)
+    monkeypatch.setattr(torch.cuda, "is_initialized", lambda: True)
     q = torch.zeros(1, 2, 4, 64, requires_grad=True)  # CPU tensors: the guard comes before the device check
     k = torch.zeros(1, 1, 4, 64, requires_grad=True)
     cos = torch.zeros(4, 32)
@@ -423,7 +423,7 @@ def test_capture_without_autograd_is_not_refused(monkeypatch):
     from nanonemo_amd.kernels.hip import flash_attn as fa
 
     monkeypatch.setattr(torch.cuda, "is_current_stream_capturing", lambda: True)
-    monkeypatch.setattr(torch.cuda, "is_available", lambda: True)
+    monkeypatch.setattr(torch.cuda, "is_initialized", lambda: True)
     q, k = torch.zeros(1, 2, 4, 64), torch.zeros(1, 1, 4, 64)
     with pytest.raises(RuntimeError, match="CUDA tensors"):
         fa.flash_attn(q, k, k)
@@ -456,7 +456,7 @@ def test_backward_ops_refuse_capture_only_inside_the_autograd_engine(monkeypatch
     from nanonemo_amd.kernels.hip import flash_attn as fa
 
     monkeypatch.setattr(torch.cuda, "is_current_stream_capturing", lambda: True)
-    monkeypatch.setattr(torch.cuda, "is_available", lambda: True)
+    monkeypatch.setattr(torch.cuda, "is_initialized", lambda: True)
     fa._refuse_capture_from_autograd_engine("outside the engine")  # returns
 
     class F(torch.autograd.Function):
