@@ -51,8 +51,9 @@ def _run(q, k, v, do):
     return o.detach().cpu(), lse.cpu(), q.grad.cpu(), k.grad.cpu(), v.grad.cpu()
 
 
-# Criterion (i) of the tolerance proposal: the kernel's error against the reference, next to PyTorch's own attention
-# in the same dtype on the same rounded inputs, measured in the same run, on max-abs and relative-Frobenius error:
+# Accuracy relative to PyTorch's own attention: the kernel's error against the reference, next to PyTorch's own
+# attention in the same dtype on the same rounded inputs, measured in the same run, on max-abs and relative-Frobenius
+# error:
 #   * at most SDPA_RATIO times the error of PyTorch's FlashAttention kernel (SDPA's flash backend, else its
 #     mem-efficient one): the same algorithm class, which like this kernel (and the reference's,
 #     /root/reference/nanonemo/kernels/cuda/flash_attn.cu:129-138,287-293) rounds P and dS to 16 bits before their
@@ -89,7 +90,7 @@ def _sdpa(q, k, v, do, backends):
 
 
 def _sdpa_bound(report, refs, inputs, label):
-    """Assert criterion (i) (see SDPA_RATIO) for o, dq, dk, dv and print the ratios."""
+    """Assert the bounds relative to PyTorch's attention (see SDPA_RATIO) for o, dq, dk, dv and print the ratios."""
     from torch.nn.attention import SDPBackend
 
     lines = []
@@ -113,8 +114,8 @@ def _sdpa_bound(report, refs, inputs, label):
 
 
 def _check(got, ref, dtype, label, inputs=None):
-    """Tolerances of tests/common.py against ``ref``; with ``inputs`` (the rounded q, k, v, dO) also criterion (i):
-    o, dq, dk, dv against PyTorch's same-dtype attention (SDPA_RATIO)."""
+    """Tolerances of tests/common.py against ``ref``; with ``inputs`` (the rounded q, k, v, dO) also the bounds
+    relative to PyTorch's same-dtype attention (SDPA_RATIO) for o, dq, dk, dv."""
     o, lse, dq, dk, dv = got
     ro, rlse, rdq, rdk, rdv = ref
     assert o.dtype == dtype and dq.dtype == dtype and dk.dtype == dtype and dv.dtype == dtype
