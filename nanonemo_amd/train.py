@@ -79,6 +79,9 @@ def run(attn: str, steps: int, batch: int, seq: int, cfg_kwargs: dict, device: s
     fresh batch per step: a stream the model can memorise, so that the loss falls and the curves have something to
     track (on uniform fresh tokens the loss stays near ln(vocab))."""
     torch.manual_seed(0)
+    attn, _, backend = attn.partition("@")  # "torch@mem_efficient": the plain attention on another SDPA backend
+    if backend:
+        cfg_kwargs = {**cfg_kwargs, "attn_backend": backend}
     kernel, *extras = attn.split("+")
     unknown = set(extras) - {"rope", "qrope", "norm"}
     if unknown:
@@ -111,7 +114,8 @@ def main():
     p.add_argument("--attn", nargs="+",
                    default=["torch", "hip", "hip_bthd", "hip_bthd+rope", "hip_bthd+rope+norm", "hip_bthd+qrope+norm"],
                    help="attention kernels; '+rope' / '+qrope' / '+norm' suffixes also select the HIP RoPE (separate / "
-                   "q folded into the attention) and add+RMSNorm kernels")
+                   "q folded into the attention) and add+RMSNorm kernels; 'torch@<backend>' runs the plain attention "
+                   "on another SDPA backend (a control for the drift between two valid attentions)")
     p.add_argument("--small", action="store_true", help="a 2-layer model (quick check)")
     p.add_argument("--distinct", type=int, default=0,
                    help="cycle through this many fixed batches (a stream the model can memorise) instead of fresh "
