@@ -194,7 +194,10 @@ def same_node(q, k, v, do, fa, reps):
     """PyTorch's own attention on the same GPU, as the reference benchmark's providers run it
     (/root/reference/benchmarks/kernels/flash_attn.py:27-49: SDPA mem-efficient and SDPA math on
     repeat_interleave'd K/V), plus SDPA's flash backend with native GQA (enable_gqa) where this PyTorch has one,
-    and this build's op through autograd the same way: fwd + autograd.grad w.r.t. q, k, v, back to back on warm
+    and this build's attention through autograd the same way (this_build_autograd: the public flash_attn, whose
+    eager path is a plain autograd.Function; this_build_autograd_ops: the custom op torch.ops.nanonemo.flash_attn
+    with its registered autograd, as torch.compile and op-level callers reach it), each as fwd + autograd.grad
+    w.r.t. q, k, v, back to back on warm
     caches; ms: time per call from HIP events, host_ms: the host's time per call in the same loop (where host_ms
     reaches ms, the host, not the GPU, sets the pace). Neither a spin kernel that holds the device while the host
     enqueues nor the profiler's kernel records give the device time of a host-paced loop faithfully here: the
@@ -225,7 +228,11 @@ def same_node(q, k, v, do, fa, reps):
     def ours():
         return torch.autograd.grad(fa.flash_attn(qs, ks, vs), (qs, ks, vs), do)
 
-    providers = {"this_build_autograd": ours, "sdpa_flash_gqa": sdpa(SDPBackend.FLASH_ATTENTION, True),
+    def ours_ops():
+        return torch.autograd.grad(torch.ops.nanonemo.flash_attn(qs, ks, vs)[0], (qs, ks, vs), do)
+
+    providers = {"this_build_autograd": ours, "this_build_autograd_ops": ours_ops,
+                 "sdpa_flash_gqa": sdpa(SDPBackend.FLASH_ATTENTION, True),
                  "sdpa_mem_efficient": sdpa(SDPBackend.EFFICIENT_ATTENTION, False)}
     if B * H * T * T <= 1 << 27:  # math materialises the B*H*T*T scores
         providers["sdpa_math"] = sdpa(SDPBackend.MATH, False)

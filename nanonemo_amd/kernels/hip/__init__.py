@@ -104,6 +104,51 @@ def lib() -> ctypes.CDLL:
     return handle
 
 
+def eager(*ts) -> bool:
+    """Whether a public function may run its eager path: a plain autograd.Function around the library call instead
+    of its torch.library op. The ops' dispatch (the dispatcher's Python kernel, the autograd.Function that
+    register_autograd generates, and a second op's dispatch in the backward) costs several tens of microseconds of
+    host time per forward + backward; the eager paths call the same launch code, so their results are the same
+    bits. True only for plain CUDA tensors outside torch.compile tracing, torch.func transforms and dispatch modes,
+    which need the ops (an opaque traced node, a transform rule, the op visible to the mode); meta and CPU tensors
+    take the ops too, whose fake impls and checks handle them."""
+    import torch
+
+    if torch.compiler.is_compiling():
+        return False
+    for t in ts:
+        if type(t) is not torch.Tensor or not t.is_cuda:
+            return False
+    return torch._C._functorch.peek_interpreter_stack() is None and not torch._C._len_torch_dispatch_stack()
+
+
+def stream_of(t) -> int:
+    """PyTorch's current HIP stream on t's device, as the hipStream_t the library takes (the handle alone, without
+    building a torch.cuda.Stream object where this PyTorch offers that)."""
+    import torch
+
+    raw = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+    if raw is not None:
+        return raw(t.device.index)
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def on_device(t):
+    """A context that makes t's device current for a launch (a no-op when it already is)."""
+    import contextlib
+
+    import torch
+
+    return contextlib.nullcontext() if t.device.index == torch.cuda.current_device() else torch.cuda.device(t.device)
+
+
+def records(*ts) -> bool:
+    """Whether autograd records a call on these inputs (grad mode on and one of them requires grad)."""
+    import torch
+
+    return torch.is_grad_enabled() and any(t.requires_grad for t in ts)
+
+
 def strides3(b: int, h: int, t: int) -> ctypes.Array:
     """An int64[3] {batch, head, row} element-stride array for the *_strided entry points."""
     return (ctypes.c_int64 * 3)(b, h, t)

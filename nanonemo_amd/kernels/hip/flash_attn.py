@@ -10,7 +10,9 @@ Differences from the reference, all widening: fp16 **and** bf16 inputs (the refe
 only, flash_attn.cu:344-346), and the compute is the HIP library behind a C ABI
 (include/nanonemo_fa.h) called through ctypes on PyTorch's current HIP stream. Every output and the
 backward workspace is allocated here by PyTorch's caching allocator; the library never allocates,
-synchronises or copies to the host, so both ops can be captured into a HIP graph.
+synchronises or copies to the host, so both ops can be captured into a HIP graph. In eager mode the public
+functions reach the same launches through a plain autograd.Function instead of the ops' dispatch, which
+halves their host time (see "the eager path" below).
 """
 
 from __future__ import annotations
@@ -20,8 +22,13 @@ import math
 
 import torch
 from torch import Tensor
+from torch.autograd.function import once_differentiable
 
 from nanonemo_amd.kernels.hip import DTYPE_BF16, DTYPE_F16, check, lib, strides3
+from nanonemo_amd.kernels.hip import eager as _eager
+from nanonemo_amd.kernels.hip import on_device as _on
+from nanonemo_amd.kernels.hip import records as _records
+from nanonemo_amd.kernels.hip import stream_of as _stream
 
 _DTYPES = {torch.float16: DTYPE_F16, torch.bfloat16: DTYPE_BF16}
 
@@ -55,8 +62,6 @@ def _check_inputs(q: Tensor, k: Tensor, v: Tensor, seq_dim: int = 2) -> None:
             raise RuntimeError("inputs must be 16-byte aligned")
 
 
-def _stream(t: Tensor) -> int:
-    return torch.cuda.current_stream(t.device).cuda_stream
 
 
 def _contig(t: Tensor) -> Tensor:
@@ -94,22 +99,37 @@ def _refuse_capture_from_autograd_engine(where: str) -> None:
         _refuse_capture_with_autograd(where)
 
 
-@torch.library.custom_op("nanonemo::flash_attn", mutates_args=())
-def _flash_attn(q: Tensor, k: Tensor, v: Tensor) -> tuple[Tensor, Tensor]:
-    q, k, v = _contig(q), _contig(k), _contig(v)
-    _check_inputs(q, k, v)
+def _launch_fwd(q: Tensor, k: Tensor, v: Tensor) -> tuple[Tensor, Tensor]:
+    """Allocates (o, lse) and launches the forward on contiguous, checked inputs."""
     B, H, T, D = q.shape
-    o = torch.empty_like(q, memory_format=torch.contiguous_format)
+    o = torch.empty_like(q)
     lse = torch.empty((B, H, T), dtype=torch.float32, device=q.device)
     if B == 0 or T == 0 or H == 0:
         return o, lse
-    with torch.cuda.device(q.device):
+    with _on(q):
         rc = lib().nn_fa_fwd(
             q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(),
             B, H, k.size(1), T, D, _DTYPES[q.dtype], 1.0 / math.sqrt(D), _stream(q),
         )
     check(rc)
     return o, lse
+
+
+def _prep(q: Tensor, k: Tensor, v: Tensor, seq_dim: int = 2) -> tuple[Tensor, Tensor, Tensor]:
+    """Contiguous copies where needed, then the checks: the forward's inputs as the launch takes them."""
+    q, k, v = _contig(q), _contig(k), _contig(v)
+    _check_inputs(q, k, v, seq_dim)
+    return q, k, v
+
+
+def _fwd(q: Tensor, k: Tensor, v: Tensor) -> tuple[Tensor, Tensor]:
+    """The forward on any strides: (o, lse)."""
+    return _launch_fwd(*_prep(q, k, v))
+
+
+@torch.library.custom_op("nanonemo::flash_attn", mutates_args=())
+def _flash_attn(q: Tensor, k: Tensor, v: Tensor) -> tuple[Tensor, Tensor]:
+    return _fwd(q, k, v)
 
 
 @_flash_attn.register_fake
@@ -121,26 +141,17 @@ def _(q, k, v):
     )
 
 
-@torch.library.custom_op("nanonemo::flash_attn_bwd", mutates_args=())
-def _flash_attn_bwd(d_o: Tensor, q: Tensor, k: Tensor, v: Tensor, o: Tensor, lse: Tensor) -> tuple[Tensor, Tensor, Tensor]:
-    d_o, q, k, v, o, lse = (_contig(t) for t in (d_o, q, k, v, o, lse))
-    _check_inputs(q, k, v)
-    if d_o.shape != q.shape or d_o.dtype != q.dtype or o.shape != q.shape or o.dtype != q.dtype:
-        raise RuntimeError("d_o must be a contiguous float16/bfloat16 tensor shaped like q")
+def _launch_bwd(d_o: Tensor, q: Tensor, k: Tensor, v: Tensor, o: Tensor, lse: Tensor) -> tuple[Tensor, Tensor, Tensor]:
+    """Allocates (dq, dk, dv) and the workspace and launches the backward on contiguous, checked inputs."""
     B, H, T, D = q.shape
     KVH = k.size(1)
-    if lse.shape != (B, H, T) or lse.dtype != torch.float32:
-        raise RuntimeError("lse must be a float32 tensor of shape (B, H, T)")
-    _refuse_capture_from_autograd_engine("flash_attn backward op")
-    dq = torch.empty_like(q, memory_format=torch.contiguous_format)
-    dk = torch.empty_like(k, memory_format=torch.contiguous_format)
-    dv = torch.empty_like(v, memory_format=torch.contiguous_format)
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
     if B == 0 or T == 0 or H == 0:
         return dq, dk, dv
     L = lib()
     ws_bytes = L.nn_fa_bwd_workspace_size(B, H, KVH, T, D)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device)
-    with torch.cuda.device(q.device):
+    with _on(q):
         rc = L.nn_fa_bwd(
             d_o.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(),
             dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), ws.data_ptr(), ws_bytes,
@@ -148,6 +159,19 @@ def _flash_attn_bwd(d_o: Tensor, q: Tensor, k: Tensor, v: Tensor, o: Tensor, lse
         )
     check(rc)
     return dq, dk, dv
+
+
+@torch.library.custom_op("nanonemo::flash_attn_bwd", mutates_args=())
+def _flash_attn_bwd(d_o: Tensor, q: Tensor, k: Tensor, v: Tensor, o: Tensor, lse: Tensor) -> tuple[Tensor, Tensor, Tensor]:
+    _refuse_capture_from_autograd_engine("flash_attn backward op")
+    d_o, q, k, v, o, lse = (_contig(t) for t in (d_o, q, k, v, o, lse))
+    _check_inputs(q, k, v)
+    if d_o.shape != q.shape or d_o.dtype != q.dtype or o.shape != q.shape or o.dtype != q.dtype:
+        raise RuntimeError("d_o must be a contiguous float16/bfloat16 tensor shaped like q")
+    B, H, T, D = q.shape
+    if lse.shape != (B, H, T) or lse.dtype != torch.float32:
+        raise RuntimeError("lse must be a float32 tensor of shape (B, H, T)")
+    return _launch_bwd(d_o, q, k, v, o, lse)
 
 
 @_flash_attn_bwd.register_fake
@@ -178,9 +202,40 @@ def _backward(ctx, d_o, _d_lse):
 _flash_attn.register_autograd(_backward, setup_context=_setup_context)
 
 
+# ---- the eager path of the public functions ----------------------------------------------------
+# The custom ops are what torch.compile traces (one opaque node each, through their fake impls) and what callers
+# of torch.ops.nanonemo.* reach. Run eagerly under autograd, an op pays for the dispatcher's Python kernel, the
+# autograd.Function that register_autograd generates and, in the backward, a second op's dispatch and checks: tens
+# of microseconds of host time per forward + backward, which at the model's shape is about the GPU time of the
+# three kernels. The public functions therefore run plain CUDA tensors in eager mode through the
+# autograd.Functions below (``eager``): the same checks and launches in the forward, and in the backward the
+# launch alone, on the contiguous inputs the forward checked and saved (the gradient autograd hands over has o's
+# shape and dtype). Outputs and gradients are the same bits as the ops'. Everything else (torch.compile tracing,
+# torch.func transforms, dispatch modes, tensor subclasses, meta and CPU tensors) goes through the custom ops.
+
+
+class _FlashAttnFn(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, q, k, v):
+        q, k, v = _prep(q, k, v)
+        o, lse = _launch_fwd(q, k, v)
+        ctx.save_for_backward(q, k, v, o, lse)
+        ctx.set_materialize_grads(False)
+        return o
+
+    @staticmethod
+    @once_differentiable
+    def backward(ctx, d_o):
+        _refuse_capture_with_autograd("flash_attn backward")
+        q, k, v, o, lse = ctx.saved_tensors
+        return _launch_bwd(_contig(_d_out(d_o, o)), q, k, v, o, lse)
+
+
 def flash_attn(q: Tensor, k: Tensor, v: Tensor) -> Tensor:
     """Causal GQA attention. q: (B, H, T, hd), k/v: (B, KVH, T, hd), fp16 or bf16, H % KVH == 0, hd in {32, 64}."""
     _refuse_capture_with_autograd("flash_attn", q, k, v)
+    if _eager(q, k, v):
+        return _FlashAttnFn.apply(q, k, v) if _records(q, k, v) else _fwd(q, k, v)[0]
     o, _ = _flash_attn(q, k, v)
     return o
 
@@ -201,23 +256,26 @@ def _bthd_strides(t: Tensor) -> ctypes.Array:
     return strides3(T * Hh * D, D, Hh * D)
 
 
-@torch.library.custom_op("nanonemo::flash_attn_bthd", mutates_args=())
-def _flash_attn_bthd(q: Tensor, k: Tensor, v: Tensor) -> tuple[Tensor, Tensor]:
-    q, k, v = _contig(q), _contig(k), _contig(v)
-    _check_inputs(q, k, v, seq_dim=1)
+def _launch_fwd_bthd(q: Tensor, k: Tensor, v: Tensor) -> tuple[Tensor, Tensor]:
+    """Allocates (o, lse) and launches the projection-layout forward on contiguous, checked inputs."""
     B, T, H, D = q.shape
-    KVH = k.size(2)
-    o = torch.empty_like(q, memory_format=torch.contiguous_format)
+    o = torch.empty_like(q)
     lse = torch.empty((B, H, T), dtype=torch.float32, device=q.device)
     if B == 0 or T == 0 or H == 0:
         return o, lse
-    with torch.cuda.device(q.device):
+    with _on(q):
         rc = lib().nn_fa_fwd_strided(
             q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(),
-            B, H, KVH, T, D, _bthd_strides(q), _bthd_strides(k), _DTYPES[q.dtype], 1.0 / math.sqrt(D), _stream(q),
+            B, H, k.size(2), T, D, _bthd_strides(q), _bthd_strides(k), _DTYPES[q.dtype], 1.0 / math.sqrt(D),
+            _stream(q),
         )
     check(rc)
     return o, lse
+
+
+@torch.library.custom_op("nanonemo::flash_attn_bthd", mutates_args=())
+def _flash_attn_bthd(q: Tensor, k: Tensor, v: Tensor) -> tuple[Tensor, Tensor]:
+    return _launch_fwd_bthd(*_prep(q, k, v, seq_dim=1))
 
 
 @_flash_attn_bthd.register_fake
@@ -229,28 +287,18 @@ def _(q, k, v):
     )
 
 
-@torch.library.custom_op("nanonemo::flash_attn_bthd_bwd", mutates_args=())
-def _flash_attn_bthd_bwd(
-    d_o: Tensor, q: Tensor, k: Tensor, v: Tensor, o: Tensor, lse: Tensor
-) -> tuple[Tensor, Tensor, Tensor]:
-    d_o, q, k, v, o, lse = (_contig(t) for t in (d_o, q, k, v, o, lse))
-    _check_inputs(q, k, v, seq_dim=1)
-    if d_o.shape != q.shape or d_o.dtype != q.dtype or o.shape != q.shape or o.dtype != q.dtype:
-        raise RuntimeError("d_o must be a contiguous float16/bfloat16 tensor shaped like q")
+def _launch_bwd_bthd(d_o: Tensor, q: Tensor, k: Tensor, v: Tensor, o: Tensor, lse: Tensor) -> tuple[Tensor, Tensor, Tensor]:
+    """Allocates (dq, dk, dv) and the workspace and launches the projection-layout backward on contiguous, checked
+    inputs."""
     B, T, H, D = q.shape
     KVH = k.size(2)
-    if lse.shape != (B, H, T) or lse.dtype != torch.float32:
-        raise RuntimeError("lse must be a float32 tensor of shape (B, H, T)")
-    _refuse_capture_from_autograd_engine("flash_attn_bthd backward op")
-    dq = torch.empty_like(q, memory_format=torch.contiguous_format)
-    dk = torch.empty_like(k, memory_format=torch.contiguous_format)
-    dv = torch.empty_like(v, memory_format=torch.contiguous_format)
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
     if B == 0 or T == 0 or H == 0:
         return dq, dk, dv
     L = lib()
     ws_bytes = L.nn_fa_bwd_workspace_size(B, H, KVH, T, D)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device)
-    with torch.cuda.device(q.device):
+    with _on(q):
         rc = L.nn_fa_bwd_strided(
             d_o.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(),
             dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), ws.data_ptr(), ws_bytes,
@@ -258,6 +306,21 @@ def _flash_attn_bthd_bwd(
         )
     check(rc)
     return dq, dk, dv
+
+
+@torch.library.custom_op("nanonemo::flash_attn_bthd_bwd", mutates_args=())
+def _flash_attn_bthd_bwd(
+    d_o: Tensor, q: Tensor, k: Tensor, v: Tensor, o: Tensor, lse: Tensor
+) -> tuple[Tensor, Tensor, Tensor]:
+    _refuse_capture_from_autograd_engine("flash_attn_bthd backward op")
+    d_o, q, k, v, o, lse = (_contig(t) for t in (d_o, q, k, v, o, lse))
+    _check_inputs(q, k, v, seq_dim=1)
+    if d_o.shape != q.shape or d_o.dtype != q.dtype or o.shape != q.shape or o.dtype != q.dtype:
+        raise RuntimeError("d_o must be a contiguous float16/bfloat16 tensor shaped like q")
+    B, T, H, D = q.shape
+    if lse.shape != (B, H, T) or lse.dtype != torch.float32:
+        raise RuntimeError("lse must be a float32 tensor of shape (B, H, T)")
+    return _launch_bwd_bthd(d_o, q, k, v, o, lse)
 
 
 @_flash_attn_bthd_bwd.register_fake
@@ -274,9 +337,32 @@ def _backward_bthd(ctx, d_o, _d_lse):
 _flash_attn_bthd.register_autograd(_backward_bthd, setup_context=_setup_context)
 
 
+class _FlashAttnBthdFn(torch.autograd.Function):
+    """The eager path of flash_attn_bthd (see flash_attn's)."""
+
+    @staticmethod
+    def forward(ctx, q, k, v):
+        q, k, v = _prep(q, k, v, seq_dim=1)
+        o, lse = _launch_fwd_bthd(q, k, v)
+        ctx.save_for_backward(q, k, v, o, lse)
+        ctx.set_materialize_grads(False)
+        return o
+
+    @staticmethod
+    @once_differentiable
+    def backward(ctx, d_o):
+        _refuse_capture_with_autograd("flash_attn_bthd backward")
+        q, k, v, o, lse = ctx.saved_tensors
+        return _launch_bwd_bthd(_contig(_d_out(d_o, o)), q, k, v, o, lse)
+
+
 def flash_attn_bthd(q: Tensor, k: Tensor, v: Tensor) -> Tensor:
     """Causal GQA attention in the projection layout: q (B, T, H, hd), k/v (B, T, KVH, hd) -> o (B, T, H, hd)."""
     _refuse_capture_with_autograd("flash_attn_bthd", q, k, v)
+    if _eager(q, k, v):
+        if _records(q, k, v):
+            return _FlashAttnBthdFn.apply(q, k, v)
+        return _launch_fwd_bthd(*_prep(q, k, v, seq_dim=1))[0]
     o, _ = _flash_attn_bthd(q, k, v)
     return o
 
@@ -302,26 +388,33 @@ def _check_tables(cos: Tensor, sin: Tensor, T: int, D: int, device: torch.device
     return _contig(cos), _contig(sin)
 
 
-@torch.library.custom_op("nanonemo::flash_attn_bthd_rope", mutates_args=())
-def _flash_attn_bthd_rope(q: Tensor, k: Tensor, v: Tensor, cos: Tensor, sin: Tensor) -> tuple[Tensor, Tensor, Tensor]:
-    q, k, v = _contig(q), _contig(k), _contig(v)
-    _check_inputs(q, k, v, seq_dim=1)
+def _prep_rope(q: Tensor, k: Tensor, v: Tensor, cos: Tensor, sin: Tensor) -> tuple[Tensor, ...]:
+    """Contiguous copies where needed and the checks of the RoPE-fused forward's inputs."""
+    q, k, v = _prep(q, k, v, seq_dim=1)
+    cos, sin = _check_tables(cos, sin, q.size(1), q.size(3), q.device)
+    return q, k, v, cos, sin
+
+
+def _launch_fwd_rope(q: Tensor, k: Tensor, v: Tensor, cos: Tensor, sin: Tensor) -> tuple[Tensor, Tensor, Tensor]:
+    """Allocates (o, lse, q_rot) and launches the RoPE-fused forward on contiguous, checked inputs."""
     B, T, H, D = q.shape
-    KVH = k.size(2)
-    cos, sin = _check_tables(cos, sin, T, D, q.device)
-    o = torch.empty_like(q, memory_format=torch.contiguous_format)
-    q_rot = torch.empty_like(q, memory_format=torch.contiguous_format)
+    o, q_rot = torch.empty_like(q), torch.empty_like(q)
     lse = torch.empty((B, H, T), dtype=torch.float32, device=q.device)
     if B == 0 or T == 0 or H == 0:
         return o, lse, q_rot
-    with torch.cuda.device(q.device):
+    with _on(q):
         rc = lib().nn_fa_fwd_rope_strided(
             q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(), q_rot.data_ptr(),
-            cos.data_ptr(), sin.data_ptr(), cos.shape[0], B, H, KVH, T, D, _bthd_strides(q), _bthd_strides(k),
+            cos.data_ptr(), sin.data_ptr(), cos.shape[0], B, H, k.size(2), T, D, _bthd_strides(q), _bthd_strides(k),
             _DTYPES[q.dtype], 1.0 / math.sqrt(D), _stream(q),
         )
     check(rc)
     return o, lse, q_rot
+
+
+@torch.library.custom_op("nanonemo::flash_attn_bthd_rope", mutates_args=())
+def _flash_attn_bthd_rope(q: Tensor, k: Tensor, v: Tensor, cos: Tensor, sin: Tensor) -> tuple[Tensor, Tensor, Tensor]:
+    return _launch_fwd_rope(*_prep_rope(q, k, v, cos, sin))
 
 
 @_flash_attn_bthd_rope.register_fake
@@ -334,29 +427,20 @@ def _(q, k, v, cos, sin):
     )
 
 
-@torch.library.custom_op("nanonemo::flash_attn_bthd_rope_bwd", mutates_args=())
-def _flash_attn_bthd_rope_bwd(
+def _launch_bwd_rope(
     d_o: Tensor, q_rot: Tensor, k: Tensor, v: Tensor, o: Tensor, lse: Tensor, cos: Tensor, sin: Tensor
 ) -> tuple[Tensor, Tensor, Tensor]:
-    d_o, q_rot, k, v, o, lse = (_contig(t) for t in (d_o, q_rot, k, v, o, lse))
-    _check_inputs(q_rot, k, v, seq_dim=1)
-    if d_o.shape != q_rot.shape or d_o.dtype != q_rot.dtype or o.shape != q_rot.shape or o.dtype != q_rot.dtype:
-        raise RuntimeError("d_o must be a contiguous float16/bfloat16 tensor shaped like q")
+    """Allocates (dq of the unrotated q, dk, dv) and the workspace and launches the RoPE-fused backward on
+    contiguous, checked inputs."""
     B, T, H, D = q_rot.shape
     KVH = k.size(2)
-    if lse.shape != (B, H, T) or lse.dtype != torch.float32:
-        raise RuntimeError("lse must be a float32 tensor of shape (B, H, T)")
-    _refuse_capture_from_autograd_engine("flash_attn_bthd_rope backward op")
-    cos, sin = _check_tables(cos, sin, T, D, q_rot.device)
-    dq = torch.empty_like(q_rot, memory_format=torch.contiguous_format)
-    dk = torch.empty_like(k, memory_format=torch.contiguous_format)
-    dv = torch.empty_like(v, memory_format=torch.contiguous_format)
+    dq, dk, dv = torch.empty_like(q_rot), torch.empty_like(k), torch.empty_like(v)
     if B == 0 or T == 0 or H == 0:
         return dq, dk, dv
     L = lib()
     ws_bytes = L.nn_fa_bwd_workspace_size(B, H, KVH, T, D)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q_rot.device)
-    with torch.cuda.device(q_rot.device):
+    with _on(q_rot):
         rc = L.nn_fa_bwd_rope_strided(
             d_o.data_ptr(), q_rot.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(),
             dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), ws.data_ptr(), ws_bytes, cos.data_ptr(), sin.data_ptr(),
@@ -365,6 +449,22 @@ def _flash_attn_bthd_rope_bwd(
         )
     check(rc)
     return dq, dk, dv
+
+
+@torch.library.custom_op("nanonemo::flash_attn_bthd_rope_bwd", mutates_args=())
+def _flash_attn_bthd_rope_bwd(
+    d_o: Tensor, q_rot: Tensor, k: Tensor, v: Tensor, o: Tensor, lse: Tensor, cos: Tensor, sin: Tensor
+) -> tuple[Tensor, Tensor, Tensor]:
+    _refuse_capture_from_autograd_engine("flash_attn_bthd_rope backward op")
+    d_o, q_rot, k, v, o, lse = (_contig(t) for t in (d_o, q_rot, k, v, o, lse))
+    _check_inputs(q_rot, k, v, seq_dim=1)
+    if d_o.shape != q_rot.shape or d_o.dtype != q_rot.dtype or o.shape != q_rot.shape or o.dtype != q_rot.dtype:
+        raise RuntimeError("d_o must be a contiguous float16/bfloat16 tensor shaped like q")
+    B, T, H, D = q_rot.shape
+    if lse.shape != (B, H, T) or lse.dtype != torch.float32:
+        raise RuntimeError("lse must be a float32 tensor of shape (B, H, T)")
+    cos, sin = _check_tables(cos, sin, T, D, q_rot.device)
+    return _launch_bwd_rope(d_o, q_rot, k, v, o, lse, cos, sin)
 
 
 @_flash_attn_bthd_rope_bwd.register_fake
@@ -390,9 +490,33 @@ def _backward_rope(ctx, d_o, _d_lse, _d_q_rot):
 _flash_attn_bthd_rope.register_autograd(_backward_rope, setup_context=_setup_context_rope)
 
 
+class _FlashAttnBthdRopeFn(torch.autograd.Function):
+    """The eager path of flash_attn_bthd_rope (see flash_attn's)."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, cos, sin):
+        q, k, v, cos, sin = _prep_rope(q, k, v, cos, sin)
+        o, lse, q_rot = _launch_fwd_rope(q, k, v, cos, sin)
+        ctx.save_for_backward(q_rot, k, v, o, lse, cos, sin)
+        ctx.set_materialize_grads(False)
+        return o
+
+    @staticmethod
+    @once_differentiable
+    def backward(ctx, d_o):
+        _refuse_capture_with_autograd("flash_attn_bthd_rope backward")
+        q_rot, k, v, o, lse, cos, sin = ctx.saved_tensors
+        dq, dk, dv = _launch_bwd_rope(_contig(_d_out(d_o, o)), q_rot, k, v, o, lse, cos, sin)
+        return dq, dk, dv, None, None
+
+
 def flash_attn_bthd_rope(q: Tensor, k: Tensor, v: Tensor, cos: Tensor, sin: Tensor) -> Tensor:
     """Causal GQA attention in the projection layout with q's RoPE folded in: q (B, T, H, hd) *before* RoPE,
     k (B, T, KVH, hd) already rotated, v (B, T, KVH, hd), cos/sin fp32 (T_max, hd/2) -> o (B, T, H, hd)."""
     _refuse_capture_with_autograd("flash_attn_bthd_rope", q, k, v)
+    if _eager(q, k, v, cos, sin):
+        if _records(q, k, v, cos, sin):
+            return _FlashAttnBthdRopeFn.apply(q, k, v, cos, sin)
+        return _launch_fwd_rope(*_prep_rope(q, k, v, cos, sin))[0]
     o, _, _ = _flash_attn_bthd_rope(q, k, v, cos, sin)
     return o

@@ -15,8 +15,10 @@ from __future__ import annotations
 
 import torch
 from torch import Tensor
+from torch.autograd.function import once_differentiable
 
-from nanonemo_amd.kernels.hip import DTYPE_BF16, DTYPE_F16, DTYPE_F32, check_rope, lib, strides3
+from nanonemo_amd.kernels.hip import DTYPE_BF16, DTYPE_F16, DTYPE_F32, check_rope, eager, lib, on_device, records
+from nanonemo_amd.kernels.hip import stream_of, strides3
 
 _DTYPES = {torch.float16: DTYPE_F16, torch.bfloat16: DTYPE_BF16, torch.float32: DTYPE_F32}
 
@@ -44,11 +46,11 @@ def _call(fn_name: str, q: Tensor, k: Tensor, cos: Tensor, sin: Tensor) -> tuple
     qo, ko = torch.empty_like(q), torch.empty_like(k)
     if q.numel() == 0 and k.numel() == 0:
         return qo, ko
-    with torch.cuda.device(q.device):
+    with on_device(q):
         rc = getattr(lib(), fn_name)(
             q.data_ptr(), qo.data_ptr(), k.data_ptr(), ko.data_ptr(), cos.data_ptr(), sin.data_ptr(),
             B, T, H, KVH, D, strides3(T * H * D, H * D, D), strides3(T * KVH * D, KVH * D, D), cos.shape[0],
-            _DTYPES[q.dtype], torch.cuda.current_stream(q.device).cuda_stream,
+            _DTYPES[q.dtype], stream_of(q),
         )
     check_rope(rc)
     return qo, ko
@@ -88,12 +90,37 @@ def _backward(ctx, dq, dk):
 _rope_qk.register_autograd(_backward, setup_context=_setup_context)
 
 
+class _RopeQkFn(torch.autograd.Function):
+    """The eager path of rope_qk (plain CUDA tensors outside tracing; ``eager``): the op's launches and autograd
+    wiring without its dispatch, so the same bits for less host time."""
+
+    @staticmethod
+    def forward(ctx, q, k, cos, sin):
+        ctx.save_for_backward(cos, sin)
+        return _call("nn_rope_qk", *_prep(q, k, cos, sin))
+
+    @staticmethod
+    @once_differentiable
+    def backward(ctx, dq, dk):
+        cos, sin = ctx.saved_tensors
+        gq, gk = _call("nn_rope_qk_bwd", *_prep(dq, dk, cos, sin))
+        return gq, gk, None, None
+
+
+def _rope(q: Tensor, k: Tensor, cos: Tensor, sin: Tensor) -> tuple[Tensor, Tensor]:
+    if eager(q, k, cos, sin):
+        if records(q, k, cos, sin):
+            return _RopeQkFn.apply(q, k, cos, sin)
+        return _call("nn_rope_qk", *_prep(q, k, cos, sin))
+    return _rope_qk(q, k, cos, sin)
+
+
 def rope_qk(q: Tensor, k: Tensor, cos: Tensor, sin: Tensor) -> tuple[Tensor, Tensor]:
     """Rotate q (B, T, H, hd) and k (B, T, KVH, hd) by the positions' angles (cos/sin: fp32 (T_max, hd/2))."""
-    return _rope_qk(q, k, cos, sin)
+    return _rope(q, k, cos, sin)
 
 
 def rope_k(k: Tensor, cos: Tensor, sin: Tensor) -> Tensor:
     """Rotate k (B, T, KVH, hd) alone (the q half of the pass is folded into the attention op)."""
     q = k.new_empty(k.shape[0], k.shape[1], 0, k.shape[3])
-    return _rope_qk(q, k, cos, sin)[1]
+    return _rope(q, k, cos, sin)[1]
