@@ -472,3 +472,16 @@ def test_backward_ops_refuse_capture_only_inside_the_autograd_engine(monkeypatch
     x = torch.ones(3, requires_grad=True)
     with pytest.raises(RuntimeError, match="inside the engine: capturing"):
         F.apply(x).sum().backward()
+
+
+def test_eager_path_routing_without_a_gpu():
+    # The public functions' eager autograd.Functions are for plain CUDA tensors only: meta and CPU tensors (and,
+    # on a GPU, transforms, dispatch modes and tracing) take the custom ops, whose fake impls and checks serve them.
+    from nanonemo_amd.kernels.hip import eager, records
+
+    meta, cpu = torch.empty(2, device="meta"), torch.zeros(2)
+    assert not eager(meta) and not eager(cpu)
+    g = torch.zeros(2, requires_grad=True)
+    assert records(cpu, g) and not records(cpu)
+    with torch.no_grad():
+        assert not records(g)
