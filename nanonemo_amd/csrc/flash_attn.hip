@@ -672,7 +672,9 @@ __global__ __launch_bounds__(256) void fa_bwd_pre_kernel(const u16* __restrict__
 // both 32-key slabs. The GQA sum over the H/KVH query heads of a KV head happens in the
 // accumulators. At the end of a unit the 4 partial dK / dV are summed through LDS and stored once
 // in the output dtype (no atomics, no fp32 round trip through HBM). A block takes unit j and unit
-// nkb-1-j, so every block carries the same causal work. When those pairs are too few to fill the
+// nkb-1-j, so every block carries the same causal work; when every unit of the problem fits on its own
+// CU and the work is not split (paired = 0), a block takes one unit instead, so that no block carries a
+// second unit's loads, iterations and reduction after its first. When the pairs are too few to fill the
 // chip, nsplit > 1 blocks share each pair: block s takes iterations [s n / nsplit, (s+1) n / nsplit)
 // of each unit (n of them) and stores its fp32 partial sums into `part` instead, which
 // fa_bwd_dkdv_sum_kernel adds in split order. Per 32-query step and 32-key slab:
@@ -686,7 +688,7 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(
     const u16* __restrict__ Q, const u16* __restrict__ K, const u16* __restrict__ V, const u16* __restrict__ dO,
     const float* __restrict__ nLvec, const float* __restrict__ nDvec, u16* __restrict__ dK, u16* __restrict__ dV,
     int BKV, int H, int KVH, int T, int nkb, int nqt, float sl2, float scale, Lay lq, Lay lk, int nsplit,
-    float* __restrict__ part) {
+    float* __restrict__ part, int paired) {
     using E = Elem<DT>;
     NN_TL_START(kTlDkdv);
     constexpr int BNK = 64, BM = 64, NW = 4, NSL = BNK / 32;
@@ -704,11 +706,11 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(
     __shared__ __attribute__((aligned(16))) float lB[NW * 2 * BM];
 
     const int nbk = (BKV + PPB - 1) / PPB;   // blocks per unit-pair index (and split)
-    const int nbase = nbk * ((nkb + 1) / 2);  // blocks of one split
+    const int nbase = nbk * (paired ? (nkb + 1) / 2 : nkb);  // blocks of one split
     const int sidx = blockIdx.x / nbase;      // this block's split
     const int bid = blockIdx.x - sidx * nbase;
     const int bgrp = bid % nbk;               // the block's pairs are (batch, KV head) bgrp PPB .. + PPB - 1
-    const int pj = bid / nbk;
+    const int pj = bid / nbk;  // the pair's first unit (the block's only unit when unpaired)
     const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
     const int wave = tid >> 6;  // a uniform copy in an SGPR costs this kernel more than it saves
     const int wp = wave % WPP;  // this wave's place among its pair's waves
@@ -776,7 +778,7 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(
     };
     // The first unit's K / V and first tiles; each later unit's are issued before the previous unit's
     // reduction, so that their latency overlaps it.
-    const int nunits = nkb - 1 - pj > pj ? 2 : 1;  // an odd unit count leaves the middle unit alone
+    const int nunits = paired && nkb - 1 - pj > pj ? 2 : 1;  // an odd unit count leaves the middle unit alone
     if (active) {
         load_kv(pj * BNK);
         const int n0 = group * (nqt - pj), i0 = first_of(n0);
@@ -1365,6 +1367,16 @@ int dkdv_waves_per_pair(int64_t B, int64_t H, int64_t KVH, int64_t T) {
     return pairs >= 3 * kDkdvFill ? 1 : (pairs >= 2 * kDkdvFill ? 2 : 4);
 }
 
+// One unit per dK/dV block instead of a pair: when the work is not split, four waves share each unit
+// and all the units fit in one block per CU (tiny problems such as B=1, T=256), a pair's second unit
+// only lengthens the block that carries it (its loads, iterations and reduction come after the
+// first's), while the CUs that a block per unit would use sit idle.
+bool dkdv_paired(int64_t B, int64_t H, int64_t KVH, int64_t T) {
+    if (B <= 0 || KVH <= 0 || H < KVH || T <= 0) return true;
+    const int64_t nkb = (T + 63) / 64;
+    return !(dkdv_split(B, H, KVH, T) == 1 && dkdv_waves_per_pair(B, H, KVH, T) == 4 && B * KVH * nkb <= kDkdvFill);
+}
+
 Workspace carve(void* base, int64_t B, int64_t H, int64_t KVH, int64_t T, int64_t D) {
     const size_t vec = round256(4 * (size_t)B * H * T);
     Workspace w;
@@ -1414,11 +1426,12 @@ int dkdv_impl(const void* q, const void* k, const void* v, const void* dO, const
     // share each pair (a block then hosts 2 or 4 pairs), so that the per-unit costs (loads, barrier,
     // reduction) are paid by fewer, longer blocks.
     const int wpp = dkdv_waves_per_pair(B, H, KVH, T);
+    const bool paired = dkdv_paired(B, H, KVH, T);
     auto launch = [&](auto kern, int ppb) {
         const int nbk = (BKV + ppb - 1) / ppb;
-        kern<<<dim3(nbk * npairs * w.nsplit), dim3(256), 0, st>>>(
+        kern<<<dim3(nbk * (paired ? npairs : nkb) * w.nsplit), dim3(256), 0, st>>>(
             (const u16*)q, (const u16*)k, (const u16*)v, (const u16*)dO, w.nL, w.nD, (u16*)dk, (u16*)dv, BKV, (int)H,
-            (int)KVH, (int)T, nkb, nqt, scale * kLog2e, scale, lq, lk, w.nsplit, w.part);
+            (int)KVH, (int)T, nkb, nqt, scale * kLog2e, scale, lq, lk, w.nsplit, w.part, paired ? 1 : 0);
     };
     if (wpp == 1)
         launch(fa_bwd_dkdv_kernel<HD, DT, 1>, 4);

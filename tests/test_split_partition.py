@@ -171,3 +171,73 @@ def test_qblock_of_covers_every_block_once_heaviest_first_per_xcd(B, H, KVH, T):
     if (BH // group) % 8 == 0:  # every query head of one (batch, KV head) group shares one XCD
         for (bh, _), bid in seen.items():
             assert (bh // group) % 8 == bid % 8
+
+
+# ---- dK/dV grid: block -> (split, waves' (batch, KV head), unit pair or single unit) -------------------
+
+
+def dkdv_waves_per_pair(B, H, KVH, T):
+    """Restates dkdv_waves_per_pair() of nanonemo_amd/csrc/flash_attn.hip."""
+    nkb = (T + 63) // 64
+    pairs = B * KVH * ((nkb + 1) // 2)
+    if (H // KVH) * (nkb + 1) > 300:
+        return 4
+    return 1 if pairs >= 3 * 256 else (2 if pairs >= 2 * 256 else 4)
+
+
+def dkdv_paired(B, H, KVH, T):
+    """Restates dkdv_paired(): one unit per block when the work is not split, four waves share each unit and all
+    the units fit in one block per CU."""
+    nkb = (T + 63) // 64
+    return not (dkdv_split(B, H, KVH, T) == 1 and dkdv_waves_per_pair(B, H, KVH, T) == 4 and B * KVH * nkb <= 256)
+
+
+def dkdv_owners(B, H, KVH, T):
+    """Every (batch * KV head, unit, iteration) the dK/dV launch's waves take, with its count: the kernel's block ->
+    (split, (batch, KV head) of each wave, first unit) mapping, its unit list and each wave's iterations
+    ifirst + wp + WPP j of the split's range."""
+    S, wpp, paired = dkdv_split(B, H, KVH, T), dkdv_waves_per_pair(B, H, KVH, T), dkdv_paired(B, H, KVH, T)
+    nkb = nqt = (T + 63) // 64
+    BKV, group, NW = B * KVH, H // KVH, 4
+    ppb = NW // wpp
+    nbk = (BKV + ppb - 1) // ppb
+    nbase = nbk * ((nkb + 1) // 2 if paired else nkb)
+    owners = {}
+    for block in range(nbase * S):
+        sidx, bid = divmod(block, nbase)
+        bgrp, pj = bid % nbk, bid // nbk
+        units = [pj] if (not paired or nkb - 1 - pj == pj) else [pj, nkb - 1 - pj]
+        for wave in range(NW):
+            wp = wave % wpp
+            bk = bgrp if wpp == NW else bgrp * ppb + wave // wpp
+            if bk >= BKV:
+                continue  # the last block's idle waves
+            for unit in units:
+                n = group * (nqt - unit)
+                first, end = sidx * n // S, (sidx + 1) * n // S
+                for itn in range(first + wp, end, wpp):
+                    owners[(bk, unit, itn)] = owners.get((bk, unit, itn), 0) + 1
+    return owners, (S, wpp, paired, nbase * S)
+
+
+@pytest.mark.parametrize(
+    "B, H, KVH, T",
+    [(1, 12, 4, 256), (4, 12, 4, 256), (16, 12, 4, 256), (32, 12, 4, 256), (8, 12, 4, 1024), (32, 12, 4, 1024),
+     (16, 12, 4, 1024), (1, 12, 4, 1024), (2, 12, 4, 8192), (8, 12, 12, 1024), (8, 12, 1, 1024), (1, 4, 4, 65),
+     (3, 6, 2, 333), (1, 1, 1, 1), (2, 8, 8, 100)],
+)
+def test_dkdv_blocks_take_every_iteration_once(B, H, KVH, T):
+    owners, (S, wpp, paired, blocks) = dkdv_owners(B, H, KVH, T)
+    nkb = nqt = (T + 63) // 64
+    want = {(bk, u, i) for bk in range(B * KVH) for u in range(nkb) for i in range((H // KVH) * (nqt - u))}
+    assert set(owners) == want and all(c == 1 for c in owners.values()), (S, wpp, paired)
+    if not paired:
+        assert S == 1 and wpp == 4 and blocks <= 256
+
+
+def test_one_unit_per_block_only_for_tiny_unsplit_problems():
+    assert not dkdv_paired(1, 12, 4, 256)  # BASELINE config 1's shape: 16 blocks of one unit instead of 8 pairs
+    assert not dkdv_paired(16, 12, 4, 256)  # 256 units, one per CU
+    assert dkdv_paired(32, 12, 4, 256)  # 512 units: pairs
+    assert dkdv_paired(8, 12, 4, 1024)  # config 2
+    assert dkdv_paired(1, 12, 4, 1024)  # split work keeps pairs
