@@ -672,10 +672,10 @@ __global__ __launch_bounds__(256) void fa_bwd_pre_kernel(const u16* __restrict__
 // both 32-key slabs. The GQA sum over the H/KVH query heads of a KV head happens in the
 // accumulators. At the end of a unit the 4 partial dK / dV are summed through LDS and stored once
 // in the output dtype (no atomics, no fp32 round trip through HBM). A block takes unit j and unit
-// nkb-1-j, so every block carries the same causal work; when every unit of the problem fits on its own
-// CU and the work is not split (paired = 0), a block takes one unit instead, so that no block carries a
-// second unit's loads, iterations and reduction after its first. When the pairs are too few to fill the
-// chip, nsplit > 1 blocks share each pair: block s takes iterations [s n / nsplit, (s+1) n / nsplit)
+// nkb-1-j, so every block carries the same causal work; small unsplit problems (paired = 0, see
+// dkdv_mode) take single units instead: one per block, or two per block with two waves each, so that no
+// block carries a second unit's loads, iterations and reduction after its first. When the pairs are too
+// few to fill the chip, nsplit > 1 blocks share each pair: block s takes iterations [s n / nsplit, (s+1) n / nsplit)
 // of each unit (n of them) and stores its fp32 partial sums into `part` instead, which
 // fa_bwd_dkdv_sum_kernel adds in split order. Per 32-query step and 32-key slab:
 //   S' = Q K^T - lse/scale, dP' = dO V^T - D   (A = Q / dO rows from LDS, B = K / V registers;
@@ -1367,14 +1367,28 @@ int dkdv_waves_per_pair(int64_t B, int64_t H, int64_t KVH, int64_t T) {
     return pairs >= 3 * kDkdvFill ? 1 : (pairs >= 2 * kDkdvFill ? 2 : 4);
 }
 
-// One unit per dK/dV block instead of a pair: when the work is not split, four waves share each unit
-// and all the units fit in one block per CU (tiny problems such as B=1, T=256), a pair's second unit
-// only lengthens the block that carries it (its loads, iterations and reduction come after the
-// first's), while the CUs that a block per unit would use sit idle.
-bool dkdv_paired(int64_t B, int64_t H, int64_t KVH, int64_t T) {
-    if (B <= 0 || KVH <= 0 || H < KVH || T <= 0) return true;
-    const int64_t nkb = (T + 63) / 64;
-    return !(dkdv_split(B, H, KVH, T) == 1 && dkdv_waves_per_pair(B, H, KVH, T) == 4 && B * KVH * nkb <= kDkdvFill);
+// Units per dK/dV block and waves per unit. A block normally takes a unit pair; when the work is not split
+// and four waves share each pair, small problems take single units instead, because a pair's second unit
+// only lengthens the block that carries it (its loads, iterations and reduction come after the first's)
+// while CUs sit idle:
+//   * all the units fit in one block per CU (B=1, T=256): one unit per block, four waves on it;
+//   * they fit in two (B=32, T=256): two units per block, two waves on each, as long as a wave's share
+//     of the heaviest unit, ceil(g nqt / 2) iterations (g query heads per KV head), stays below a pair
+//     wave's share, about ceil(g (nqt + 1) / 4), plus the unit change between the pair's units, which
+//     costs about kDkdvUnitChangeIters iterations' time (its loop-end spread and reduction). Measured:
+//     10-23 % faster at T <= 256, 9 % slower at B=16, T=512, where the rule keeps pairs.
+struct DkdvMode {
+    bool paired;
+    int wpp;  // waves per pair, or per unit when unpaired
+};
+constexpr int64_t kDkdvUnitChangeIters = 3;
+DkdvMode dkdv_mode(int64_t B, int64_t H, int64_t KVH, int64_t T) {
+    const int wpp = dkdv_waves_per_pair(B, H, KVH, T);
+    if (B <= 0 || KVH <= 0 || H < KVH || T <= 0 || dkdv_split(B, H, KVH, T) != 1 || wpp != 4) return {true, wpp};
+    const int64_t nkb = (T + 63) / 64, units = B * KVH * nkb, g = H / KVH;
+    if (units <= kDkdvFill) return {false, 4};
+    if (units <= 2 * kDkdvFill && (g * nkb + 1) / 2 < (g * (nkb + 1) + 3) / 4 + kDkdvUnitChangeIters) return {false, 2};
+    return {true, 4};
 }
 
 Workspace carve(void* base, int64_t B, int64_t H, int64_t KVH, int64_t T, int64_t D) {
@@ -1425,8 +1439,9 @@ int dkdv_impl(const void* q, const void* k, const void* v, const void* dO, const
     // Waves per unit pair: 4 while the pairs do not fill two blocks per CU; with more pairs, fewer waves
     // share each pair (a block then hosts 2 or 4 pairs), so that the per-unit costs (loads, barrier,
     // reduction) are paid by fewer, longer blocks.
-    const int wpp = dkdv_waves_per_pair(B, H, KVH, T);
-    const bool paired = dkdv_paired(B, H, KVH, T);
+    const DkdvMode mode = dkdv_mode(B, H, KVH, T);
+    const int wpp = mode.wpp;
+    const bool paired = mode.paired;
     auto launch = [&](auto kern, int ppb) {
         const int nbk = (BKV + ppb - 1) / ppb;
         kern<<<dim3(nbk * (paired ? npairs : nkb) * w.nsplit), dim3(256), 0, st>>>(

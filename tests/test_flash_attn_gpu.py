@@ -323,6 +323,19 @@ def test_fewer_waves_per_unit_pair_matches_oracle(B, H, KVH, T, hd):
     _check(_run(q, k, v, do), _oracle(q, k, v, do), dtype, f"waves per pair {(B, H, KVH, T, hd)}")
 
 
+# Small unsplit shapes whose dK/dV blocks take single units (B * KVH * ceil(T / 64) units): one per block (config
+# 1's shape, 16 units), or two per block with two waves each (512 and 396 units; the second leaves two waves of its
+# last block idle).
+SINGLE_UNITS = [(1, 12, 4, 256, 64, torch.bfloat16), (32, 12, 4, 256, 64, torch.bfloat16),
+                (33, 3, 3, 256, 32, torch.float16), (64, 12, 4, 128, 64, torch.float16)]
+
+
+@pytest.mark.parametrize("B, H, KVH, T, hd, dtype", SINGLE_UNITS)
+def test_single_unit_dkdv_blocks_match_oracle(B, H, KVH, T, hd, dtype):
+    q, k, v, do = make_inputs(B, H, KVH, T, hd, dtype, seed=17)
+    _check(_run(q, k, v, do), _oracle(q, k, v, do), dtype, f"single units {(B, H, KVH, T, hd, dtype)}")
+
+
 # A plain shape, an fp16 head_dim-32 MQA shape whose dK/dV work is split, and a bf16 split shape.
 SEPARATE = [(2, 12, 4, 300, 64, torch.bfloat16), (1, 12, 1, 700, 32, torch.float16), (2, 12, 1, 1024, 64, torch.bfloat16)]
 

@@ -185,18 +185,32 @@ def dkdv_waves_per_pair(B, H, KVH, T):
     return 1 if pairs >= 3 * 256 else (2 if pairs >= 2 * 256 else 4)
 
 
-def dkdv_paired(B, H, KVH, T):
-    """Restates dkdv_paired(): one unit per block when the work is not split, four waves share each unit and all
-    the units fit in one block per CU."""
+def dkdv_mode(B, H, KVH, T):
+    """Restates dkdv_mode(): (paired, waves per pair or unit). Unsplit four-wave problems take single units when
+    they fit in one block per CU (four waves each) or in two (two waves each) while a wave's share of the heaviest
+    unit stays below a pair wave's share plus a unit change (3 iterations)."""
+    wpp = dkdv_waves_per_pair(B, H, KVH, T)
+    if dkdv_split(B, H, KVH, T) != 1 or wpp != 4:
+        return True, wpp
     nkb = (T + 63) // 64
-    return not (dkdv_split(B, H, KVH, T) == 1 and dkdv_waves_per_pair(B, H, KVH, T) == 4 and B * KVH * nkb <= 256)
+    units, g = B * KVH * nkb, H // KVH
+    if units <= 256:
+        return False, 4
+    if units <= 512 and (g * nkb + 1) // 2 < (g * (nkb + 1) + 3) // 4 + 3:
+        return False, 2
+    return True, 4
+
+
+def dkdv_paired(B, H, KVH, T):
+    return dkdv_mode(B, H, KVH, T)[0]
 
 
 def dkdv_owners(B, H, KVH, T):
     """Every (batch * KV head, unit, iteration) the dK/dV launch's waves take, with its count: the kernel's block ->
     (split, (batch, KV head) of each wave, first unit) mapping, its unit list and each wave's iterations
     ifirst + wp + WPP j of the split's range."""
-    S, wpp, paired = dkdv_split(B, H, KVH, T), dkdv_waves_per_pair(B, H, KVH, T), dkdv_paired(B, H, KVH, T)
+    S = dkdv_split(B, H, KVH, T)
+    paired, wpp = dkdv_mode(B, H, KVH, T)
     nkb = nqt = (T + 63) // 64
     BKV, group, NW = B * KVH, H // KVH, 4
     ppb = NW // wpp
@@ -223,6 +237,7 @@ def dkdv_owners(B, H, KVH, T):
 @pytest.mark.parametrize(
     "B, H, KVH, T",
     [(1, 12, 4, 256), (4, 12, 4, 256), (16, 12, 4, 256), (32, 12, 4, 256), (8, 12, 4, 1024), (32, 12, 4, 1024),
+     (64, 12, 4, 128), (24, 12, 4, 256), (8, 12, 12, 256), (33, 3, 3, 256), (16, 12, 4, 512),
      (16, 12, 4, 1024), (1, 12, 4, 1024), (2, 12, 4, 8192), (8, 12, 12, 1024), (8, 12, 1, 1024), (1, 4, 4, 65),
      (3, 6, 2, 333), (1, 1, 1, 1), (2, 8, 8, 100)],
 )
@@ -232,12 +247,14 @@ def test_dkdv_blocks_take_every_iteration_once(B, H, KVH, T):
     want = {(bk, u, i) for bk in range(B * KVH) for u in range(nkb) for i in range((H // KVH) * (nqt - u))}
     assert set(owners) == want and all(c == 1 for c in owners.values()), (S, wpp, paired)
     if not paired:
-        assert S == 1 and wpp == 4 and blocks <= 256
+        assert S == 1 and blocks <= 256 and (wpp == 4 or wpp == 2)
 
 
-def test_one_unit_per_block_only_for_tiny_unsplit_problems():
-    assert not dkdv_paired(1, 12, 4, 256)  # BASELINE config 1's shape: 16 blocks of one unit instead of 8 pairs
-    assert not dkdv_paired(16, 12, 4, 256)  # 256 units, one per CU
-    assert dkdv_paired(32, 12, 4, 256)  # 512 units: pairs
-    assert dkdv_paired(8, 12, 4, 1024)  # config 2
-    assert dkdv_paired(1, 12, 4, 1024)  # split work keeps pairs
+def test_single_units_only_for_small_unsplit_problems():
+    assert dkdv_mode(1, 12, 4, 256) == (False, 4)  # BASELINE config 1's shape: 16 blocks of one unit, not 8 pairs
+    assert dkdv_mode(16, 12, 4, 256) == (False, 4)  # 256 units, one per CU
+    assert dkdv_mode(32, 12, 4, 256) == (False, 2)  # 512 units, two per block (the ladder's T=256 point)
+    assert dkdv_mode(64, 12, 4, 128) == (False, 2)
+    assert dkdv_mode(16, 12, 4, 512) == (True, 4)  # 512 units, but a wave's share of unit 0 (12) is too long
+    assert dkdv_mode(8, 12, 4, 1024) == (True, 4)  # config 2
+    assert dkdv_mode(1, 12, 4, 1024)[0]  # split work keeps pairs
