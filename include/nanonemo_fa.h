@@ -149,6 +149,15 @@ int nn_fa_bwd_noalloc(const void* dO, const void* q, const void* k, const void* 
                       int64_t B, int64_t H, int64_t KVH, int64_t T, int64_t D,
                       int dtype, float scale, void* stream);
 
+/* The backward's dK/dV launch plan for a shape, computed on the host (no GPU, no allocation), for inspection
+ * and tests: *nsplit blocks share each unit pair's iterations (above 1: fp32 partials in the workspace and a
+ * sum kernel), *waves waves share a pair (or a unit), *paired is 1 when a block takes a pair of 64-key
+ * units (j and nkb - 1 - j) and 0 when it takes single units (small unsplit problems), *blocks is the grid.
+ * Returns 0, or nonzero with nn_fa_last_error set for sizes the library rejects. No counterpart in the
+ * reference (its backward launch, flash_attn.cu:393-401, has one fixed grid). */
+int nn_fa_bwd_plan(int64_t B, int64_t H, int64_t KVH, int64_t T, int* nsplit, int* waves, int* paired,
+                   int64_t* blocks);
+
 /* Message of the last failed call on this thread ("" if none). Replaces the TORCH_CHECK
  * messages of flash_attn.cu:342-356 and :383-385. */
 const char* nn_fa_last_error(void);

@@ -1382,6 +1382,12 @@ struct DkdvMode {
     int wpp;  // waves per pair, or per unit when unpaired
 };
 constexpr int64_t kDkdvUnitChangeIters = 3;
+// The dK/dV grid: blocks of 4 waves, each wave on the (batch, KV head) of its pair or unit (4 / wpp of them per
+// block), times the pairs or units of one (batch, KV head), times the splits.
+int64_t dkdv_blocks(int64_t B, int64_t KVH, int64_t T, DkdvMode mode, int nsplit) {
+    const int64_t nkb = (T + 63) / 64, ppb = 4 / mode.wpp, nbk = (B * KVH + ppb - 1) / ppb;
+    return nbk * (mode.paired ? (nkb + 1) / 2 : nkb) * nsplit;
+}
 DkdvMode dkdv_mode(int64_t B, int64_t H, int64_t KVH, int64_t T) {
     const int wpp = dkdv_waves_per_pair(B, H, KVH, T);
     if (B <= 0 || KVH <= 0 || H < KVH || T <= 0 || dkdv_split(B, H, KVH, T) != 1 || wpp != 4) return {true, wpp};
@@ -1443,8 +1449,7 @@ int dkdv_impl(const void* q, const void* k, const void* v, const void* dO, const
     const int wpp = mode.wpp;
     const bool paired = mode.paired;
     auto launch = [&](auto kern, int ppb) {
-        const int nbk = (BKV + ppb - 1) / ppb;
-        kern<<<dim3(nbk * (paired ? npairs : nkb) * w.nsplit), dim3(256), 0, st>>>(
+        kern<<<dim3((unsigned)dkdv_blocks(B, KVH, T, mode, w.nsplit)), dim3(256), 0, st>>>(
             (const u16*)q, (const u16*)k, (const u16*)v, (const u16*)dO, w.nL, w.nD, (u16*)dk, (u16*)dv, BKV, (int)H,
             (int)KVH, (int)T, nkb, nqt, scale * kLog2e, scale, lq, lk, w.nsplit, w.part, paired ? 1 : 0);
     };
@@ -1454,6 +1459,7 @@ int dkdv_impl(const void* q, const void* k, const void* v, const void* dO, const
         launch(fa_bwd_dkdv_kernel<HD, DT, 2>, 2);
     else
         launch(fa_bwd_dkdv_kernel<HD, DT, 4>, 1);
+    (void)npairs;
     if (int e = launch_status("fa_bwd_dkdv_kernel")) return e;
     if (w.nsplit == 1) return 0;
     const int64_t n4 = 2 * (int64_t)BKV * T * HD / 4;
@@ -1518,11 +1524,24 @@ int check_ws(void* workspace, size_t workspace_bytes, int64_t B, int64_t H, int6
 
 NNFA_API const char* nn_fa_last_error(void) { return g_last_error.c_str(); }
 
-NNFA_API int nn_fa_abi_version(void) { return 9; }
+NNFA_API int nn_fa_abi_version(void) { return 10; }
 
 NNFA_API size_t nn_fa_bwd_workspace_size(int64_t B, int64_t H, int64_t KVH, int64_t T, int64_t D) {
     if (B < 0 || H < 0 || KVH < 0 || T < 0 || D < 0) return 0;
     return carve(nullptr, B, H, KVH, T, D).bytes;
+}
+
+NNFA_API int nn_fa_bwd_plan(int64_t B, int64_t H, int64_t KVH, int64_t T, int* nsplit, int* waves, int* paired,
+                            int64_t* blocks) {
+    g_last_error.clear();
+    if (!nsplit || !waves || !paired || !blocks) return fail(-1, "nn_fa_bwd_plan: null output pointer");
+    if (int e = check_dims(B, H, KVH, T, 64, kBF16)) return e;
+    const DkdvMode mode = dkdv_mode(B, H, KVH, T);
+    *nsplit = dkdv_split(B, H, KVH, T);
+    *waves = mode.wpp;
+    *paired = mode.paired ? 1 : 0;
+    *blocks = B == 0 || T == 0 ? 0 : dkdv_blocks(B, KVH, T, mode, *nsplit);
+    return 0;
 }
 
 namespace {

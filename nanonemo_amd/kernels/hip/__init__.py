@@ -62,6 +62,9 @@ SIGNATURES: dict[str, tuple] = {
     "nn_fa_bwd_noalloc": (
         _int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _int, _f32, _vp]
     ),
+    "nn_fa_bwd_plan": (
+        _int, [_i64, _i64, _i64, _i64, ctypes.POINTER(_int), ctypes.POINTER(_int), ctypes.POINTER(_int), _i64p]
+    ),
     "nn_fa_last_error": (ctypes.c_char_p, []),
     "nn_fa_abi_version": (_int, []),
     # include/nanonemo_rope.h
@@ -83,7 +86,7 @@ SIGNATURES: dict[str, tuple] = {
     "nn_rmsnorm_last_error": (ctypes.c_char_p, []),
 }
 
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 
 @cache

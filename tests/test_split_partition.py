@@ -258,3 +258,36 @@ def test_single_units_only_for_small_unsplit_problems():
     assert dkdv_mode(16, 12, 4, 512) == (True, 4)  # 512 units, but a wave's share of unit 0 (12) is too long
     assert dkdv_mode(8, 12, 4, 1024) == (True, 4)  # config 2
     assert dkdv_mode(1, 12, 4, 1024)[0]  # split work keeps pairs
+
+
+@pytest.mark.parametrize(
+    "B, H, KVH, T",
+    [(1, 12, 4, 256), (16, 12, 4, 256), (32, 12, 4, 256), (64, 12, 4, 128), (16, 12, 4, 512), (8, 12, 4, 1024),
+     (32, 12, 4, 1024), (2, 12, 4, 8192), (1, 12, 4, 16384), (16, 12, 4, 1024), (65, 4, 2, 700), (91, 2, 1, 700),
+     (2, 12, 1, 1024), (1, 12, 2, 700), (33, 3, 3, 256), (8, 12, 12, 256), (1, 1, 1, 1), (0, 12, 4, 256), (4, 8, 8, 0)],
+)
+def test_library_plan_matches_the_mirrors(B, H, KVH, T):
+    # The library's own launch decisions (nn_fa_bwd_plan, computed on the host) are what the emulations above
+    # restate: the same splits, waves, pairing and grid.
+    import ctypes
+
+    n, w, p, g = ctypes.c_int(), ctypes.c_int(), ctypes.c_int(), ctypes.c_int64()
+    assert lib().nn_fa_bwd_plan(B, H, KVH, T, ctypes.byref(n), ctypes.byref(w), ctypes.byref(p), ctypes.byref(g)) == 0
+    if B == 0 or T == 0:
+        assert g.value == 0
+        return
+    paired, wpp = dkdv_mode(B, H, KVH, T)
+    assert (n.value, w.value, bool(p.value)) == (dkdv_split(B, H, KVH, T), wpp, paired)
+    nkb, ppb = (T + 63) // 64, 4 // wpp
+    assert g.value == -(-B * KVH // ppb) * ((nkb + 1) // 2 if paired else nkb) * n.value
+    if B * KVH * T <= 1 << 16:  # and the grid the block-mapping emulation walks
+        assert g.value == dkdv_owners(B, H, KVH, T)[1][3]
+
+
+def test_library_plan_rejects_bad_sizes():
+    import ctypes
+
+    n, w, p, g = ctypes.c_int(), ctypes.c_int(), ctypes.c_int(), ctypes.c_int64()
+    assert lib().nn_fa_bwd_plan(1, 12, 5, 64, ctypes.byref(n), ctypes.byref(w), ctypes.byref(p), ctypes.byref(g)) != 0
+    assert b"group evenly" in lib().nn_fa_last_error()
+    assert lib().nn_fa_bwd_plan(1, 12, 4, 64, None, ctypes.byref(w), ctypes.byref(p), ctypes.byref(g)) != 0
