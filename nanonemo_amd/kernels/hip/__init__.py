@@ -122,7 +122,12 @@ def eager(*ts) -> bool:
     for t in ts:
         if type(t) is not torch.Tensor or not t.is_cuda:
             return False
-    return torch._C._functorch.peek_interpreter_stack() is None and not torch._C._len_torch_dispatch_stack()
+    # Both queries are PyTorch internals; where this PyTorch lacks one, the ops take every call.
+    transforms = getattr(getattr(torch._C, "_functorch", None), "peek_interpreter_stack", None)
+    modes = getattr(torch._C, "_len_torch_dispatch_stack", None)
+    if transforms is None or modes is None:
+        return False
+    return transforms() is None and not modes()
 
 
 def stream_of(t) -> int:
