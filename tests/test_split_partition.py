@@ -201,10 +201,6 @@ def dkdv_mode(B, H, KVH, T):
     return True, 4
 
 
-def dkdv_paired(B, H, KVH, T):
-    return dkdv_mode(B, H, KVH, T)[0]
-
-
 def dkdv_owners(B, H, KVH, T):
     """Every (batch * KV head, unit, iteration) the dK/dV launch's waves take, with its count: the kernel's block ->
     (split, (batch, KV head) of each wave, first unit) mapping, its unit list and each wave's iterations
