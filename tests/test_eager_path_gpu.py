@@ -186,3 +186,20 @@ def test_add_rms_norm_eager_path_matches_the_op_bit_for_bit(with_delta, autocast
     assert type(ra[0].grad_fn).__name__.startswith("_AddRmsNormFn")
     for i, (p, r) in enumerate(zip(ra, rb)):
         assert torch.equal(p, r), f"output {i}: max |diff| {(p.float() - r.float()).abs().max().item()}"
+
+
+def test_eager_path_under_activation_checkpointing():
+    # torch.utils.checkpoint runs the forward again inside the backward: the gradients equal a plain run's, bit for
+    # bit (the kernels are deterministic).
+    from torch.utils.checkpoint import checkpoint
+
+    from nanonemo_amd.kernels.hip import flash_attn as fa
+
+    g = torch.Generator(device="cpu").manual_seed(19)
+    q, do = (torch.randn(2, 300, 8, 64, generator=g).bfloat16().to(DEV) for _ in range(2))
+    k, v = (torch.randn(2, 300, 2, 64, generator=g).bfloat16().to(DEV) for _ in range(2))
+    a, b = _leaves(q, k, v), _leaves(q, k, v)
+    ga = torch.autograd.grad(fa.flash_attn_bthd(*a), a, do)
+    gb = torch.autograd.grad(checkpoint(fa.flash_attn_bthd, *b, use_reentrant=False), b, do)
+    for x, y in zip(ga, gb):
+        assert torch.equal(x, y)
