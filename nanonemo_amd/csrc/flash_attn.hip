@@ -683,7 +683,11 @@ __global__ __launch_bounds__(256) void fa_bwd_pre_kernel(const u16* __restrict__
 //   P = exp2(S' * sl2), dS = P dP'
 //   dV^T += dO^T P, dK^T += Q^T dS             (A = columns of the Q / dO tiles, B = P / dS registers)
 // ------------------------------------------------------------------------------------------
-template <int HD, int DT, int WPP>
+// KVL: with four waves on one unit pair (WPP = 4), the block copies each unit's K and V rows once into LDS
+// (each wave a quarter, by DMA), and every wave reads its K / V operands from there, instead of each wave
+// loading all 64 rows from memory; the second unit's rows are copied a whole unit ahead, while the first
+// unit's loop runs, so its unit change carries only the first tiles' copies.
+template <int HD, int DT, int WPP, bool KVL>
 __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(
     const u16* __restrict__ Q, const u16* __restrict__ K, const u16* __restrict__ V, const u16* __restrict__ dO,
     const float* __restrict__ nLvec, const float* __restrict__ nDvec, u16* __restrict__ dK, u16* __restrict__ dV,
@@ -704,6 +708,8 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(
     __shared__ __attribute__((aligned(16))) u16 oB[NW * QT];
     __shared__ __attribute__((aligned(16))) float lA[NW * 2 * BM];  // per wave: -lse/scale | -D
     __shared__ __attribute__((aligned(16))) float lB[NW * 2 * BM];
+    static_assert(!KVL || WPP == NW, "K / V through LDS needs the block's four waves on one pair");
+    __shared__ __attribute__((aligned(16))) u16 kvS[KVL ? 2 * BNK * HD : 8];  // a unit's K rows, then its V rows
 
     const int nbk = (BKV + PPB - 1) / PPB;   // blocks per unit-pair index (and split)
     const int nbase = nbk * (paired ? (nkb + 1) / 2 : nkb);  // blocks of one split
@@ -751,6 +757,22 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(
             }
         }
     };
+    // KVL: this wave's quarter of a unit's K and V rows into kvS (swizzled like the Q / dO tiles), and every
+    // wave's operands from there.
+    const DmaOffs<HD, BNK, NW> kvo = dma_offsets<HD, BNK, NW>(lane, wave, lk.st);
+    auto issue_kv = [&](int kb0_) {
+        dma_rows<HD, BNK, NW>(K + kvoff, lk.st, kb0_, T, kvS, wave, kvo);
+        dma_rows<HD, BNK, NW>(V + kvoff, lk.st, kb0_, T, kvS + BNK * HD, wave, kvo);
+    };
+    auto read_kv = [&]() {
+#pragma unroll
+        for (int sl = 0; sl < NSL; ++sl)
+#pragma unroll
+            for (int s = 0; s < NS; ++s) {
+                kf[sl][s] = ld8(kvS + 32 * sl * HD + qroff[s]);
+                vf[sl][s] = ld8(kvS + BNK * HD + 32 * sl * HD + qroff[s]);
+            }
+    };
     // Iteration itn of unit qtf (whose query tiles run from qtf to nqt - 1): query head iter_head of the group,
     // query tile iter_tile. Head-minor, so that the group's diagonal iterations, which carry the mask, go to
     // different waves. The pair's first unit (pj, the longer) walks its tiles down from the last one, the second
@@ -777,9 +799,23 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(
         __builtin_amdgcn_global_load_lds(reinterpret_cast<const char*>(nDvec + ro + q0) + lo, LDS_AS(void, ls + wu * 2 * BM + BM), 4, 0, 0);
     };
     // The first unit's K / V and first tiles; each later unit's are issued before the previous unit's
-    // reduction, so that their latency overlaps it.
+    // reduction, so that their latency overlaps it. With KVL (and two units) the first unit's rows go through
+    // kvS, and once every wave has read them the second unit's rows are copied there; rows past T read as
+    // zeros, where the direct loads repeat row T - 1 (both are future keys of every row, masked below).
     const int nunits = paired && nkb - 1 - pj > pj ? 2 : 1;  // an odd unit count leaves the middle unit alone
-    if (active) {
+    const bool kvl = KVL && nunits == 2;  // block-uniform (with WPP = 4 the block's waves share one pair)
+    if (kvl) {
+        if (active) {
+            issue_kv(pj * BNK);
+            const int n0 = group * (nqt - pj), i0 = first_of(n0);
+            if (wp < end_of(n0) - i0) issue_it(i0 + wp, pj, qA, oA, lA);
+        }
+        wait_vmem();
+        __syncthreads();
+        if (active) read_kv();
+        barrier_lds();  // every wave's reads of kvS are done before the second unit's copies overwrite it
+        if (active) issue_kv((nkb - 1 - pj) * BNK);
+    } else if (active) {
         load_kv(pj * BNK);
         const int n0 = group * (nqt - pj), i0 = first_of(n0);
         if (wp < end_of(n0) - i0) issue_it(i0 + wp, pj, qA, oA, lA);
@@ -788,6 +824,11 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(
     for (int ui = 0; ui < nunits; ++ui) {
         const int unit = ui == 0 ? pj : nkb - 1 - pj;
         const int kb0 = unit * BNK;
+        if (kvl && ui == 1) {  // the second unit's rows, copied during the first unit's loop, into registers
+            wait_vmem();
+            __syncthreads();
+            if (active) read_kv();
+        }
         const int qt_first = unit, nq = nqt - qt_first, niter = group * nq;
         const int ifirst = first_of(niter), nsp = end_of(niter) - ifirst;  // this split's iterations
         const int nmine = active && wp < nsp ? (nsp - wp + WPP - 1) / WPP : 0;  // iterations ifirst + wp + WPP j
@@ -936,7 +977,13 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(
         // have returned, which their use by the MFMAs guarantees.
         for (int j = 0; j < nmine; j += 2) {  // iteration ifirst + wp is already in flight into buffer A
             const int itn = ifirst + wp + WPP * j;
-            wait_vmem();  // this iteration's tiles, copied during the previous one
+            // This iteration's tiles, copied during the previous one. The first time with KVL, the second unit's K / V
+            // copies, issued after the tiles, stay in flight.
+            constexpr int kKvOps = 2 * (BNK * HD / 8) / (64 * NW);
+            if (kvl && ui == 0 && j == 0)
+                wait_vmem_keep<kKvOps>();
+            else
+                wait_vmem();
             if (ui == 0 && j == 0) NN_TL_BLOCK(kTlDkdv, kTlMtReady, __builtin_amdgcn_s_memtime());
             if (j + 1 < nmine)
                 run(std::true_type{}, itn, qA, oA, lA, itn + WPP, qB, oB, lB);
@@ -951,13 +998,14 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(
         }
 
         // This wave is done with its tiles, its copies have landed (its last iteration issued none) and
-        // its K / V registers are free: it issues the next unit's K / V loads and first tiles (into its A
-        // slots) now, while it waits for the slower waves, and they stay in flight through the reduction,
-        // which uses only the B buffers. The next unit's loop waits for them (vmcnt) before reading either.
+        // its K / V registers are free: it issues the next unit's K / V loads (with KVL: already in kvS) and
+        // first tiles (into its A slots) now, while it waits for the slower waves, and they stay in flight
+        // through the reduction, which uses only the B buffers. The next unit's loop waits for them (vmcnt)
+        // before reading either.
         if (ui < 2) NN_TL_WAVE(kTlDkdv, kTlExtra + 4 * ui + wave, __builtin_amdgcn_s_memtime());
         if (ui + 1 < nunits && active) {
             const int un = nkb - 1 - pj;
-            load_kv(un * BNK);
+            if (!kvl) load_kv(un * BNK);
             const int n1 = group * (nqt - un), i1 = first_of(n1);
             if (wp < end_of(n1) - i1) issue_it(i1 + wp, un, qA, oA, lA);
         }
@@ -1453,12 +1501,16 @@ int dkdv_impl(const void* q, const void* k, const void* v, const void* dO, const
             (const u16*)q, (const u16*)k, (const u16*)v, (const u16*)dO, w.nL, w.nD, (u16*)dk, (u16*)dv, BKV, (int)H,
             (int)KVH, (int)T, nkb, nqt, scale * kLog2e, scale, lq, lk, w.nsplit, w.part, paired ? 1 : 0);
     };
+    // K / V through LDS (KVL) for pairs at head_dim 64 up to T = 2048: measured 1-3.4 % faster there (config 2:
+    // -3 %), within noise or slower at T >= 4096 and at head_dim 32, where the direct loads stay.
     if (wpp == 1)
-        launch(fa_bwd_dkdv_kernel<HD, DT, 1>, 4);
+        launch(fa_bwd_dkdv_kernel<HD, DT, 1, false>, 4);
     else if (wpp == 2)
-        launch(fa_bwd_dkdv_kernel<HD, DT, 2>, 2);
+        launch(fa_bwd_dkdv_kernel<HD, DT, 2, false>, 2);
+    else if (HD == 64 && paired && nkb <= 32)
+        launch(fa_bwd_dkdv_kernel<HD, DT, 4, true>, 1);
     else
-        launch(fa_bwd_dkdv_kernel<HD, DT, 4>, 1);
+        launch(fa_bwd_dkdv_kernel<HD, DT, 4, false>, 1);
     (void)npairs;
     if (int e = launch_status("fa_bwd_dkdv_kernel")) return e;
     if (w.nsplit == 1) return 0;
