@@ -1502,12 +1502,13 @@ int dkdv_impl(const void* q, const void* k, const void* v, const void* dO, const
             (int)KVH, (int)T, nkb, nqt, scale * kLog2e, scale, lq, lk, w.nsplit, w.part, paired ? 1 : 0);
     };
     // K / V through LDS (KVL) for pairs at head_dim 64 up to T = 2048: measured 1-3.4 % faster there (config 2:
-    // -3 %), within noise or slower at T >= 4096 and at head_dim 32, where the direct loads stay.
+    // -3 %), within noise or slower at T >= 4096 and at head_dim 32, where the direct loads stay. The timeline
+    // build keeps the direct loads everywhere: with its clock stamps the KVL instantiation spills registers.
     if (wpp == 1)
         launch(fa_bwd_dkdv_kernel<HD, DT, 1, false>, 4);
     else if (wpp == 2)
         launch(fa_bwd_dkdv_kernel<HD, DT, 2, false>, 2);
-    else if (HD == 64 && paired && nkb <= 32)
+    else if (HD == 64 && paired && nkb <= 32 && !NN_TIMELINE)
         launch(fa_bwd_dkdv_kernel<HD, DT, 4, true>, 1);
     else
         launch(fa_bwd_dkdv_kernel<HD, DT, 4, false>, 1);
