@@ -1017,11 +1017,15 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(
         // which only it used in its loop and the next unit's first tiles leave alone: a wave stages as soon
         // as its loop is done, and with one wave per pair no wave waits for another. The LDS-only barriers
         // leave the next unit's loads in flight.
-        // Without a split the owner rounds the sums to 16 bits and writes them back into its own slot of
-        // the chunk (dK in the first half, dV in the second: 32 rows of 16 bytes, row r at 16-byte group
-        // (r + j) % 32 with j = the chunk's 16-byte column group, so that the groups of one gradient row
-        // fall in different banks); then the pair's waves store whole gradient rows, 16 bytes per lane.
-        // With a split the owner stores its fp32 sums into the split's partial directly.
+        // Without a split and with four waves on the pair, the owner rounds its sums to 16 bits and stores them
+        // straight from registers (each store instruction covers 16 bytes of 32 gradient rows; measured 1-3 %
+        // faster than the transpose below, which costs an LDS round trip and a barrier). With fewer waves per
+        // pair a wave owns more chunks, and the transpose pays (direct stores: 2-4 % slower there): the owner
+        // writes its 16-bit sums back into its own slot of the chunk (dK in the first half, dV in the second:
+        // 32 rows of 16 bytes, row r at 16-byte group (r + j) % 32 with j = the chunk's 16-byte column group,
+        // so that the groups of one gradient row fall in different banks); then the pair's waves store whole
+        // gradient rows, 16 bytes per lane. With a split the owner stores its fp32 sums into the split's partial
+        // directly.
         constexpr int NCK = NSL * ND * 4;
         constexpr int NG = HD / 8;  // 16-byte (8-column) groups per 16-bit gradient row
         static_assert(NCK / 2 * 1024 == QT * 2, "a wave's chunks fill its two B tile slots");
@@ -1055,7 +1059,12 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(
                     for (int m = 0; m < WPP; ++m)
                         sum += m == P ? chunk(c) : reinterpret_cast<const f32x4*>(slot(wave - P + m, c))[lane];
                     sum *= mul;
-                    if (nsplit == 1) {
+                    if (nsplit == 1 && WPP == NW) {  // the owner stores its 16-bit sums straight from registers
+                        const int key = kb0 + 32 * (c / (4 * ND)) + l32, col = 32 * (c / 4 % ND) + 8 * (c % 4) + 4 * hh;
+                        if (active && key < T)
+                            *reinterpret_cast<u32x2*>((which == 0 ? dK : dV) + kvoff + (size_t)key * lk.st + col) =
+                                u32x2{E::pack2(sum[0], sum[1]), E::pack2(sum[2], sum[3])};
+                    } else if (nsplit == 1) {
                         reinterpret_cast<u32x2*>(row16(wave, c, which, l32))[hh] =
                             u32x2{E::pack2(sum[0], sum[1]), E::pack2(sum[2], sum[3])};
                     } else {  // this split's partial: part[split][dK | dV][bk][key][HD]
@@ -1082,7 +1091,7 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(
         };
         reduce(dk, scale, 0);
         reduce(dv, 1.f, 1);
-        if (nsplit == 1) {
+        if (nsplit == 1 && WPP != NW) {
             // The pair's 64 x HD sums of each gradient: 64 NG groups of 16 bytes, 64 NG / WPP per wave.
 #pragma unroll
             for (int k = 0; k < NG / WPP; ++k) {
@@ -1502,13 +1511,12 @@ int dkdv_impl(const void* q, const void* k, const void* v, const void* dO, const
             (int)KVH, (int)T, nkb, nqt, scale * kLog2e, scale, lq, lk, w.nsplit, w.part, paired ? 1 : 0);
     };
     // K / V through LDS (KVL) for pairs at head_dim 64 up to T = 2048: measured 1-3.4 % faster there (config 2:
-    // -3 %), within noise or slower at T >= 4096 and at head_dim 32, where the direct loads stay. The timeline
-    // build keeps the direct loads everywhere: with its clock stamps the KVL instantiation spills registers.
+    // -3 %), within noise or slower at T >= 4096 and at head_dim 32, where the direct loads stay.
     if (wpp == 1)
         launch(fa_bwd_dkdv_kernel<HD, DT, 1, false>, 4);
     else if (wpp == 2)
         launch(fa_bwd_dkdv_kernel<HD, DT, 2, false>, 2);
-    else if (HD == 64 && paired && nkb <= 32 && !NN_TIMELINE)
+    else if (HD == 64 && paired && nkb <= 32)
         launch(fa_bwd_dkdv_kernel<HD, DT, 4, true>, 1);
     else
         launch(fa_bwd_dkdv_kernel<HD, DT, 4, false>, 1);
