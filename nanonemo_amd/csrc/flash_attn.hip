@@ -824,7 +824,10 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(
     for (int ui = 0; ui < nunits; ++ui) {
         const int unit = ui == 0 ? pj : nkb - 1 - pj;
         const int kb0 = unit * BNK;
-        if (kvl && ui == 1) {  // the second unit's rows, copied during the first unit's loop, into registers
+        // The second unit's rows, copied during the first unit's loop, into registers. With KVL a second unit
+        // implies kvl; the test is on KVL and ui > 0 so that the compiler sees every later unit redefine the K / V
+        // registers, and does not keep the previous unit's alive through its reduction.
+        if (KVL && ui > 0) {
             wait_vmem();
             __syncthreads();
             if (active) read_kv();
@@ -1005,7 +1008,9 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(
         if (ui < 2) NN_TL_WAVE(kTlDkdv, kTlExtra + 4 * ui + wave, __builtin_amdgcn_s_memtime());
         if (ui + 1 < nunits && active) {
             const int un = nkb - 1 - pj;
-            if (!kvl) load_kv(un * BNK);
+            // With KVL a unit change implies two units, i.e. kvl: the next unit's K / V are in kvS already.
+            // (Compile-time, so that the K / V registers are free through the reduction.)
+            if constexpr (!KVL) load_kv(un * BNK);
             const int n1 = group * (nqt - un), i1 = first_of(n1);
             if (wp < end_of(n1) - i1) issue_it(i1 + wp, un, qA, oA, lA);
         }
@@ -1051,27 +1056,56 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(
                         if (c % 4 % WPP != P) reinterpret_cast<f32x4*>(slot(wave, c))[lane] = chunk(c);
                     barrier_lds();
                 }
+                // The owned chunks: c = 4 i + P + WPP j (j < 4 / WPP). Every staged copy they need is read first,
+                // then all the sums are formed, then stored: one block of code with no branch, so that the LDS
+                // reads are in flight together and wait once. (Read and summed chunk by chunk between the stores,
+                // whose bounds tests are branches, every read waited alone: dK/dV 1-5 % slower.)
+                constexpr int GPW = 4 / WPP, NO = NCK / WPP;
+                auto owned = [](int k) { return 4 * (k / GPW) + P + WPP * (k % GPW); };
+                f32x4 copy[NO][WPP];
 #pragma unroll
-                for (int c = 0; c < NCK; ++c) {
-                    if (c % 4 % WPP != P) continue;
-                    f32x4 sum = {0.f, 0.f, 0.f, 0.f};
+                for (int k = 0; k < NO; ++k)
 #pragma unroll
                     for (int m = 0; m < WPP; ++m)
-                        sum += m == P ? chunk(c) : reinterpret_cast<const f32x4*>(slot(wave - P + m, c))[lane];
-                    sum *= mul;
-                    if (nsplit == 1 && WPP == NW) {  // the owner stores its 16-bit sums straight from registers
-                        const int key = kb0 + 32 * (c / (4 * ND)) + l32, col = 32 * (c / 4 % ND) + 8 * (c % 4) + 4 * hh;
-                        if (active && key < T)
-                            *reinterpret_cast<u32x2*>((which == 0 ? dK : dV) + kvoff + (size_t)key * lk.st + col) =
-                                u32x2{E::pack2(sum[0], sum[1]), E::pack2(sum[2], sum[3])};
-                    } else if (nsplit == 1) {
-                        reinterpret_cast<u32x2*>(row16(wave, c, which, l32))[hh] =
-                            u32x2{E::pack2(sum[0], sum[1]), E::pack2(sum[2], sum[3])};
-                    } else {  // this split's partial: part[split][dK | dV][bk][key][HD]
-                        const int key = kb0 + 32 * (c / (4 * ND)) + l32, col = 32 * (c / 4 % ND) + 8 * (c % 4) + 4 * hh;
+                        if (m != P) copy[k][m] = reinterpret_cast<const f32x4*>(slot(wave - P + m, owned(k)))[lane];
+                f32x4 sum[NO];
+#pragma unroll
+                for (int k = 0; k < NO; ++k) {
+                    // In wave order, starting from the pair's first wave's partial (0 + x is x: the partials are
+                    // never -0, an MFMA chain from +0 cannot produce it).
+                    sum[k] = P == 0 ? chunk(owned(k)) : copy[k][0];
+#pragma unroll
+                    for (int m = 1; m < WPP; ++m) sum[k] += m == P ? chunk(owned(k)) : copy[k][m];
+                    sum[k] *= mul;
+                }
+                auto col_of = [&](int c) { return 32 * (c / 4 % ND) + 8 * (c % 4) + 4 * hh; };
+                if (nsplit == 1 && WPP == NW) {  // the owner stores its 16-bit sums straight from registers
+#pragma unroll
+                    for (int sl = 0; sl < NSL; ++sl) {
+                        const int key = kb0 + 32 * sl + l32;
                         if (active && key < T) {
-                            float* dst = part + (((size_t)sidx * 2 + which) * BKV + bk) * T * HD + (size_t)key * HD + col;
-                            *reinterpret_cast<f32x4*>(dst) = sum;
+                            u16* row = (which == 0 ? dK : dV) + kvoff + (size_t)key * lk.st;
+#pragma unroll
+                            for (int k = 0; k < NO; ++k)
+                                if (owned(k) / (4 * ND) == sl)
+                                    *reinterpret_cast<u32x2*>(row + col_of(owned(k))) =
+                                        u32x2{E::pack2(sum[k][0], sum[k][1]), E::pack2(sum[k][2], sum[k][3])};
+                        }
+                    }
+                } else if (nsplit == 1) {
+#pragma unroll
+                    for (int k = 0; k < NO; ++k)
+                        reinterpret_cast<u32x2*>(row16(wave, owned(k), which, l32))[hh] =
+                            u32x2{E::pack2(sum[k][0], sum[k][1]), E::pack2(sum[k][2], sum[k][3])};
+                } else {  // this split's partial: part[split][dK | dV][bk][key][HD]
+#pragma unroll
+                    for (int sl = 0; sl < NSL; ++sl) {
+                        const int key = kb0 + 32 * sl + l32;
+                        if (active && key < T) {
+                            float* row = part + (((size_t)sidx * 2 + which) * BKV + bk) * T * HD + (size_t)key * HD;
+#pragma unroll
+                            for (int k = 0; k < NO; ++k)
+                                if (owned(k) / (4 * ND) == sl) *reinterpret_cast<f32x4*>(row + col_of(owned(k))) = sum[k];
                         }
                     }
                 }
