@@ -418,22 +418,24 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_kernel(const u16* __restrict__ 
         dma_rows<HD, BN, NW>(Kp, lk.st, it * BN, T, kb, wave, dfo);
         dma_rows<HD, BN, NW>(Vp, lk.st, it * BN, T, vb, wave, dfo);
     };
+    // Per-lane LDS offsets of a row operand (row l32 of a 32-row slice, columns 16ks + 8hh; add 32t*HD).
+    int koff[NS];
+#pragma unroll
+    for (int ks = 0; ks < NS; ++ks) koff[ks] = row_off<HD>(l32, 16 * ks + 8 * hh);
+    // The first K / V tile, then this wave's 32 Q rows by DMA into its slice of the second K tile buffer, which
+    // the loop's first copy overwrites only after the block barrier (whole 128-byte rows per 8 lanes; loaded
+    // per lane in the operand layout, each load instruction would touch 32 rows 32 bytes at a time). Rows past
+    // T read as zeros: their scores stay finite and nothing of theirs is stored.
+    issue(0, kA, vA);
+    if (qw < T) {
+        const DmaOffs<HD, 32, 1> rfo = dma_offsets<HD, 32, 1>(lane, 0, lq.st);
+        dma_rows<HD, 32, 1>(Q + qoff, lq.st, qw, T, kB + 32 * wave * HD, 0, rfo);
+    }
     u16x8 qf[NS];
     if constexpr (ROPE) {
-        // Rows past T load row T - 1 (their scores stay finite and nothing of theirs is stored): unconditional
-        // loads, which the compiler keeps in flight together.
-        const int qc = min(qrow, T - 1);
-#pragma unroll
-        for (int s = 0; s < NS; ++s) qf[s] = ld8(Q + qoff + (size_t)qc * lq.st + 16 * s + 8 * hh);
-    } else {
-#pragma unroll
-        for (int s = 0; s < NS; ++s) qf[s] = qrow < T ? ld8(Q + qoff + (size_t)qrow * lq.st + 16 * s + 8 * hh) : u16x8{};
-    }
-    if constexpr (ROPE) {
-        // The row's cos / sin values are loaded with the Q rows and the first K / V tile copy is issued with
-        // them, before the rotation, so that the three latencies overlap. The rotated rows are stored to q_rot
-        // at the end, with O: vector-memory counts complete in order, so a store issued earlier would make the
-        // next tile's wait wait for it.
+        // The row's cos / sin values are loaded with the Q rows and the first K / V tile, before the rotation,
+        // so that the latencies overlap. The rotated rows are stored to q_rot at the end, with O: vector-memory
+        // counts complete in order, so a store issued earlier would make the next tile's wait wait for it.
         // qf[s] holds columns 16 s + 8 hh .. + 7 of the row, so qf[s] and qf[s + NS / 2] are the two halves of
         // the same rotation pairs (columns c and c + HD / 2, c < HD / 2).
         constexpr int HALF = HD / 2;
@@ -447,7 +449,9 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_kernel(const u16* __restrict__ 
                 cs[s][x] = *reinterpret_cast<const f32x4*>(cr + 16 * s + 8 * hh + 4 * x);
                 sn[s][x] = *reinterpret_cast<const f32x4*>(sr + 16 * s + 8 * hh + 4 * x);
             }
-        issue(0, kA, vA);
+        wait_vmem();
+#pragma unroll
+        for (int s = 0; s < NS; ++s) qf[s] = ld8(kB + 32 * wave * HD + koff[s]);
         {
 #pragma unroll
             for (int s = 0; s < NS / 2; ++s) {
@@ -465,6 +469,10 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_kernel(const u16* __restrict__ 
                 qf[s + NS / 2] = __builtin_bit_cast(u16x8, w2);
             }
         }
+    } else {
+        wait_vmem();
+#pragma unroll
+        for (int s = 0; s < NS; ++s) qf[s] = ld8(kB + 32 * wave * HD + koff[s]);
     }
 
     f32x16 oacc[ND];
@@ -473,11 +481,9 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_kernel(const u16* __restrict__ 
     float mb = -INFINITY, lsum = 0.f;
     bool first = true;  // wave-uniform: no sub-tile processed yet
 
-    // Per-lane LDS offsets: K row operand (key l32 + 32t, columns 16ks + 8hh; add 32t*HD) and
-    // V^T column operand (keys 16c + 8x + 4hh.., column 32dt + l32; add 16c*HD).
-    int koff[NS], voff[ND][2];
-#pragma unroll
-    for (int ks = 0; ks < NS; ++ks) koff[ks] = row_off<HD>(l32, 16 * ks + 8 * hh);
+    // Per-lane LDS offsets of a V^T column operand (keys 16c + 8x + 4hh.., column 32dt + l32; add 16c*HD); K row
+    // operands (key l32 + 32t) use koff.
+    int voff[ND][2];
 #pragma unroll
     for (int dt = 0; dt < ND; ++dt)
 #pragma unroll
@@ -594,7 +600,6 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_kernel(const u16* __restrict__ 
             tile(std::false_type{}, k0, kb, vb);
     };
 
-    if constexpr (!ROPE) issue(0, kA, vA);
     for (int it = 0; it < ntiles; it += 2) {
         wait_vmem();
         __syncthreads();
@@ -1203,6 +1208,7 @@ __global__ __launch_bounds__(256, 2) void fa_bwd_dq_kernel(const u16* __restrict
     __shared__ __attribute__((aligned(16))) u16 vA[TILE];
     __shared__ __attribute__((aligned(16))) u16 kB[TILE];
     __shared__ __attribute__((aligned(16))) u16 vB[TILE];
+    __shared__ __attribute__((aligned(16))) u16 oS[BM * HD];  // the block's O rows (for D)
 
     const QBlk blk = qblock_of(blockIdx.x, BH, H / KVH, nqb);
     const int bh = blk.bh, qb = blk.qb;
@@ -1220,28 +1226,6 @@ __global__ __launch_bounds__(256, 2) void fa_bwd_dq_kernel(const u16* __restrict
     const int q0 = qb * BM, qw = q0 + wave * 32, qrow = qw + l32;
     const int qc_ = min(qrow, T - 1);
 
-    // The preprocessing pass, for this block's rows: D = rowsum(dO * O) from the 16-bit O (each half-wave
-    // holds half of a row; one exchange completes it), and -lse/scale. Every query row belongs to exactly
-    // one dQ block, which also writes both into the workspace for the dK/dV kernel that runs next.
-    u16x8 qf[NS], gf[NS];
-    float dacc = 0.f;
-#pragma unroll
-    for (int s = 0; s < NS; ++s) {
-        qf[s] = ld8(Q + qoff + (size_t)qc_ * lq.st + 16 * s + 8 * hh);
-        gf[s] = ld8(dO + qoff + (size_t)qc_ * lq.st + 16 * s + 8 * hh);
-        const u16x8 of = ld8(O + qoff + (size_t)qc_ * lq.st + 16 * s + 8 * hh);
-#pragma unroll
-        for (int j = 0; j < 8; ++j) dacc = fmaf(E::to_f32(gf[s][j]), E::to_f32(of[j]), dacc);
-    }
-    const float nd = -pair_sum(dacc);
-    const float lse = LSE[(size_t)bh * T + qc_];
-    const float nl2 = -lse * kLog2e;  // (-lse/scale) * sl2
-    if (hh == 0 && qrow < T) {
-        nDvec[(size_t)bh * T + qrow] = nd;
-        nLvec[(size_t)bh * T + qrow] = -lse / scale;
-    }
-    NN_TL_BLOCK(kTlDq, kTlExtra, __builtin_amdgcn_s_memtime());
-
     int koff[NS], kcol[ND][2];
 #pragma unroll
     for (int ks = 0; ks < NS; ++ks) koff[ks] = row_off<HD>(l32, 16 * ks + 8 * hh);
@@ -1249,6 +1233,43 @@ __global__ __launch_bounds__(256, 2) void fa_bwd_dq_kernel(const u16* __restrict
     for (int dt = 0; dt < ND; ++dt)
 #pragma unroll
         for (int x = 0; x < 2; ++x) kcol[dt][x] = col_off<HD>(8 * x + 4 * hh, 32 * dt + 16 * g16, lane);
+    auto issue = [&](int it, u16* kb, u16* vb) {
+        dma_rows<HD, BT, NW>(Kp, lk.st, it * BT, T, kb, wave, dfo);
+        dma_rows<HD, BT, NW>(Vp, lk.st, it * BT, T, vb, wave, dfo);
+    };
+    // The first K / V tile, then this wave's 32 Q, dO and O rows by DMA (whole 128-byte rows per 8 lanes;
+    // loaded per lane in the operand layout, each load instruction would touch 32 rows 32 bytes at a time):
+    // Q and dO into its slices of the second tile buffers, which the loop's first copy overwrites only after
+    // the block barrier, O into oS. Rows past T read as zeros.
+    issue(0, kA, vA);
+    const float lse = LSE[(size_t)bh * T + qc_];
+    if (qw < T) {
+        const DmaOffs<HD, 32, 1> rfo = dma_offsets<HD, 32, 1>(lane, 0, lq.st);
+        dma_rows<HD, 32, 1>(Q + qoff, lq.st, qw, T, kB + 32 * wave * HD, 0, rfo);
+        dma_rows<HD, 32, 1>(dO + qoff, lq.st, qw, T, vB + 32 * wave * HD, 0, rfo);
+        dma_rows<HD, 32, 1>(O + qoff, lq.st, qw, T, oS + 32 * wave * HD, 0, rfo);
+    }
+    wait_vmem();
+    // The preprocessing pass, for this block's rows: D = rowsum(dO * O) from the 16-bit O (each half-wave
+    // holds half of a row; one exchange completes it), and -lse/scale. Every query row belongs to exactly
+    // one dQ block, which also writes both into the workspace for the dK/dV kernel that runs next.
+    u16x8 qf[NS], gf[NS];
+    float dacc = 0.f;
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+        qf[s] = ld8(kB + 32 * wave * HD + koff[s]);
+        gf[s] = ld8(vB + 32 * wave * HD + koff[s]);
+        const u16x8 of = ld8(oS + 32 * wave * HD + koff[s]);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) dacc = fmaf(E::to_f32(gf[s][j]), E::to_f32(of[j]), dacc);
+    }
+    const float nd = -pair_sum(dacc);
+    const float nl2 = -lse * kLog2e;  // (-lse/scale) * sl2
+    if (hh == 0 && qrow < T) {
+        nDvec[(size_t)bh * T + qrow] = nd;
+        nLvec[(size_t)bh * T + qrow] = -lse / scale;
+    }
+    NN_TL_BLOCK(kTlDq, kTlExtra, __builtin_amdgcn_s_memtime());
 
     f32x16 dq[ND];
 #pragma unroll
@@ -1256,10 +1277,6 @@ __global__ __launch_bounds__(256, 2) void fa_bwd_dq_kernel(const u16* __restrict
 
     const int ntiles = (min(q0 + BM, T) + BT - 1) / BT;
     NN_TL_BLOCK(kTlDq, kTlExtra + 1, (unsigned long long)ntiles);
-    auto issue = [&](int it, u16* kb, u16* vb) {
-        dma_rows<HD, BT, NW>(Kp, lk.st, it * BT, T, kb, wave, dfo);
-        dma_rows<HD, BT, NW>(Vp, lk.st, it * BT, T, vb, wave, dfo);
-    };
     // -D enters as the initial value of every dP^T accumulator (the same for all of a lane's keys).
     f32x16 ndv;
 #pragma unroll
@@ -1322,7 +1339,6 @@ __global__ __launch_bounds__(256, 2) void fa_bwd_dq_kernel(const u16* __restrict
         half(it * BT + BN, kb + BN * HD, vb + BN * HD);
     };
 
-    issue(0, kA, vA);
     for (int it = 0; it < ntiles; it += 2) {
         wait_vmem();
         __syncthreads();
