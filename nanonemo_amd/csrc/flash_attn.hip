@@ -804,26 +804,44 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(
         __builtin_amdgcn_global_load_lds(reinterpret_cast<const char*>(nDvec + ro + q0) + lo, LDS_AS(void, ls + wu * 2 * BM + BM), 4, 0, 0);
     };
     // The first unit's K / V and first tiles; each later unit's are issued before the previous unit's
-    // reduction, so that their latency overlaps it. With KVL (and two units) the first unit's rows go through
-    // kvS, and once every wave has read them the second unit's rows are copied there; rows past T read as
-    // zeros, where the direct loads repeat row T - 1 (both are future keys of every row, masked below).
+    // reduction, so that their latency overlaps it. With KVL the first unit's rows go through kvS and, with two
+    // units, once every wave has read them the second unit's rows are copied there, in flight during the first
+    // unit's loop; rows past T read as zeros, where the direct loads repeat row T - 1 (both are future keys of
+    // every row, masked below). KVL takes kvS for a single unit too: then no register the loops read comes
+    // from a global load, which would make the compiler wait for every copy in flight (the second unit's K / V
+    // included) before it enters the unit loop.
     const int nunits = paired && nkb - 1 - pj > pj ? 2 : 1;  // an odd unit count leaves the middle unit alone
     const bool kvl = KVL && nunits == 2;  // block-uniform (with WPP = 4 the block's waves share one pair)
-    if (kvl) {
+    // The partial dK^T / dV^T of the current unit, cleared while the first copies are in flight and again after
+    // each unit's reduction.
+    f32x16 dk[NSL][ND], dv[NSL][ND];
+    auto clear_acc = [&]() {
+#pragma unroll
+        for (int sl = 0; sl < NSL; ++sl)
+#pragma unroll
+            for (int dt = 0; dt < ND; ++dt) dk[sl][dt] = dv[sl][dt] = f32x16{};
+    };
+    if constexpr (KVL) {
         if (active) {
             issue_kv(pj * BNK);
             const int n0 = group * (nqt - pj), i0 = first_of(n0);
             if (wp < end_of(n0) - i0) issue_it(i0 + wp, pj, qA, oA, lA);
         }
+        clear_acc();
         wait_vmem();
         __syncthreads();
         if (active) read_kv();
-        barrier_lds();  // every wave's reads of kvS are done before the second unit's copies overwrite it
-        if (active) issue_kv((nkb - 1 - pj) * BNK);
-    } else if (active) {
-        load_kv(pj * BNK);
-        const int n0 = group * (nqt - pj), i0 = first_of(n0);
-        if (wp < end_of(n0) - i0) issue_it(i0 + wp, pj, qA, oA, lA);
+        if (kvl) {
+            barrier_lds();  // every wave's reads of kvS are done before the second unit's copies overwrite it
+            if (active) issue_kv((nkb - 1 - pj) * BNK);
+        }
+    } else {
+        if (active) {
+            load_kv(pj * BNK);
+            const int n0 = group * (nqt - pj), i0 = first_of(n0);
+            if (wp < end_of(n0) - i0) issue_it(i0 + wp, pj, qA, oA, lA);
+        }
+        clear_acc();
     }
 
     for (int ui = 0; ui < nunits; ++ui) {
@@ -841,11 +859,6 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(
         const int ifirst = first_of(niter), nsp = end_of(niter) - ifirst;  // this split's iterations
         const int nmine = active && wp < nsp ? (nsp - wp + WPP - 1) / WPP : 0;  // iterations ifirst + wp + WPP j
 
-        f32x16 dk[NSL][ND], dv[NSL][ND];
-#pragma unroll
-        for (int sl = 0; sl < NSL; ++sl)
-#pragma unroll
-            for (int dt = 0; dt < ND; ++dt) dk[sl][dt] = dv[sl][dt] = f32x16{};
 
         // Iteration itn -> 64-row query tile.
         auto qbase_of = [&](int itn) { return iter_tile(itn, qt_first) * BM; };
@@ -1148,6 +1161,7 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(
             if constexpr (WPP > 1) barrier_lds();  // the B buffers are free for the next unit
         }
         if (ui == 0) NN_TL_BLOCK(kTlDkdv, kTlExtra + 8, __builtin_amdgcn_s_memtime());
+        if (ui + 1 < nunits) clear_acc();
     }
     NN_TL_END(kTlDkdv);
 }
