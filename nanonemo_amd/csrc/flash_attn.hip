@@ -814,13 +814,21 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(
     const bool kvl = KVL && nunits == 2;  // block-uniform (with WPP = 4 the block's waves share one pair)
     // The partial dK^T / dV^T of the current unit, cleared once before the unit loop and again after each unit's
     // reduction. (Declared and cleared at the top of the unit loop, they cost about twice as many register moves
-    // there: dK/dV 2-4 % slower.)
+    // there: dK/dV 2-4 % slower.) Each accumulator is cleared by an MFMA of zero operands onto a zero C, one
+    // instruction per 16 registers on the matrix pipe; the empty asm statements keep the compiler from seeing
+    // the operands as constants, which would let it compute one zero tile and copy it 16 registers at a time.
     f32x16 dk[NSL][ND], dv[NSL][ND];
     auto clear_acc = [&]() {
 #pragma unroll
         for (int sl = 0; sl < NSL; ++sl)
 #pragma unroll
-            for (int dt = 0; dt < ND; ++dt) dk[sl][dt] = dv[sl][dt] = f32x16{};
+            for (int dt = 0; dt < ND; ++dt) {
+                u16x8 zk = {}, zv = {};
+                __asm__ volatile("" : "+v"(zk));
+                __asm__ volatile("" : "+v"(zv));
+                dk[sl][dt] = E::mfma(zk, zk, f32x16{});
+                dv[sl][dt] = E::mfma(zv, zv, f32x16{});
+            }
     };
     if constexpr (KVL) {
         if (active) {
