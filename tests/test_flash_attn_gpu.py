@@ -336,6 +336,37 @@ def test_single_unit_dkdv_blocks_match_oracle(B, H, KVH, T, hd, dtype):
     _check(_run(q, k, v, do), _oracle(q, k, v, do), dtype, f"single units {(B, H, KVH, T, hd, dtype)}")
 
 
+# Paired dK/dV blocks with four waves whose K / V rows go through LDS (head_dim 64, at most 32 units per head)
+# and an odd unit count, so that the middle block carries one unit alone (it takes its K / V through LDS too):
+# 15 and 31 units per head. Against the float32 reference on the GPU (the float64 oracle is slow at these sizes).
+KVL_ODD = [(8, 12, 4, 960, 64, torch.bfloat16), (4, 12, 4, 1984, 64, torch.float16)]
+
+
+@pytest.mark.parametrize("B, H, KVH, T, hd, dtype", KVL_ODD)
+def test_paired_kv_through_lds_with_a_middle_unit(B, H, KVH, T, hd, dtype):
+    import ctypes
+
+    from nanonemo_amd.kernels.hip import lib
+
+    n, w, p, g = ctypes.c_int(), ctypes.c_int(), ctypes.c_int(), ctypes.c_int64()
+    assert lib().nn_fa_bwd_plan(B, H, KVH, T, ctypes.byref(n), ctypes.byref(w), ctypes.byref(p), ctypes.byref(g)) == 0
+    assert (n.value, w.value, p.value) == (1, 4, 1), (n.value, w.value, p.value)  # unsplit, paired, 4 waves
+    print(f"\n[case] paired K/V-through-LDS dK/dV with a middle unit {(B, H, KVH, T, hd, dtype)}", flush=True)
+    torch.manual_seed(21)
+    q, do = (torch.randn(B, H, T, hd, device=DEV).to(dtype) for _ in range(2))
+    k, v = (torch.randn(B, KVH, T, hd, device=DEV).to(dtype) for _ in range(2))
+    fa = _fa()
+    qs, ks, vs = (t.clone().requires_grad_() for t in (q, k, v))
+    o, lse = fa._flash_attn(qs, ks, vs)
+    dq, dk, dv = torch.autograd.grad(o, (qs, ks, vs), do)
+    got = (o.detach(), lse, dq, dk, dv)
+    ref = _torch_fp32_reference(q, k, v, do)
+    _check(tuple(t.cpu() for t in got), tuple(t.cpu() for t in ref), dtype, f"kvl odd {(B, H, KVH, T, hd, dtype)}",
+           inputs=(q, k, v, do))
+    del ref
+    torch.cuda.empty_cache()
+
+
 # A plain shape, an fp16 head_dim-32 MQA shape whose dK/dV work is split, and a bf16 split shape.
 SEPARATE = [(2, 12, 4, 300, 64, torch.bfloat16), (1, 12, 1, 700, 32, torch.float16), (2, 12, 1, 1024, 64, torch.bfloat16)]
 
