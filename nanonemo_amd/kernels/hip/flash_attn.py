@@ -62,8 +62,6 @@ def _check_inputs(q: Tensor, k: Tensor, v: Tensor, seq_dim: int = 2) -> None:
             raise RuntimeError("inputs must be 16-byte aligned")
 
 
-
-
 def _contig(t: Tensor) -> Tensor:
     return t if t.is_contiguous() else t.contiguous()
 
