@@ -803,6 +803,7 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(
         __builtin_amdgcn_global_load_lds(reinterpret_cast<const char*>(nLvec + ro + q0) + lo, LDS_AS(void, ls + wu * 2 * BM), 4, 0, 0);
         __builtin_amdgcn_global_load_lds(reinterpret_cast<const char*>(nDvec + ro + q0) + lo, LDS_AS(void, ls + wu * 2 * BM + BM), 4, 0, 0);
     };
+    constexpr int kDmaOps = 2 * (QT / 8 / 64) + 2;  // vector-memory instructions per issue_it()
     // The first unit's K / V and first tiles; each later unit's are issued before the previous unit's
     // reduction, so that their latency overlaps it. With KVL the first unit's rows go through kvS and, with two
     // units, once every wave has read them the second unit's rows are copied there, in flight during the first
@@ -831,14 +832,24 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(
             }
     };
     if constexpr (KVL) {
+        bool tile0 = false;  // wave-uniform: this wave's first tiles were issued after its K / V copies
         if (active) {
             issue_kv(pj * BNK);
             const int n0 = group * (nqt - pj), i0 = first_of(n0);
-            if (wp < end_of(n0) - i0) issue_it(i0 + wp, pj, qA, oA, lA);
+            if (wp < end_of(n0) - i0) {
+                issue_it(i0 + wp, pj, qA, oA, lA);
+                tile0 = true;
+            }
         }
         clear_acc();
-        wait_vmem();
-        __syncthreads();
+        // This wave's K / V copies have landed (copies complete in issue order; its first tiles may stay in
+        // flight), and after the barrier every wave's have. An LDS-only barrier: __syncthreads would wait for the
+        // tiles too.
+        if (tile0)
+            wait_vmem_keep<kDmaOps>();
+        else
+            wait_vmem();
+        barrier_lds();
         if (active) read_kv();
         if (kvl) {
             barrier_lds();  // every wave's reads of kvS are done before the second unit's copies overwrite it
@@ -913,7 +924,6 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(
         // one, their copy instructions spread over the MFMAs (the CU's copy path accepts them only so
         // fast, and an in-order wave that issued them back to back would stall on it with its MFMA
         // pipe idle).
-        constexpr int kDmaOps = 2 * (QT / 8 / 64) + 2;  // vector-memory instructions per issue()
         auto compute = [&](auto mask_tag, auto dma_tag, int qbase, const u16* qs, const u16* os, const float* ls,
                            int nitn, u16* nqs, u16* nos, float* nls) {
             constexpr bool MASK = decltype(mask_tag)::value;
