@@ -288,6 +288,21 @@ __device__ inline void dma_rows(const u16* __restrict__ g, int ld, int r0, int T
 #endif
 }
 
+// 64 consecutive fp32 values g[0 .. 63] into LDS (lane l's value at lds[l]) by one buffer-load DMA, lane l
+// reading g[off_l / 4] (off_l in bytes, below 256). A buffer load, like the tiles' copies, rather than a global
+// one: the compiler counts a global load to LDS also among the LDS operations, whose waits it then cannot count
+// per instruction, and every LDS wait after one (through the next loop iteration) becomes a wait for all.
+__device__ inline void dma_vec64(const float* __restrict__ g, uint32_t off, float* lds) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    const uint64_t ga = reinterpret_cast<uint64_t>(g);
+    const uint32_t ghi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(ga >> 32));
+    const uint32_t glo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)ga);
+    void* gt = reinterpret_cast<void*>(((uint64_t)ghi << 32) | glo);
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(gt, 0, 256, kBufWord3);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, LDS_AS(void, lds), 4, off, 0, 0, 0);
+#endif
+}
+
 // Block -> (batch * H + head, query block) for the forward and dQ grids of nqb * BH blocks: heaviest
 // query blocks first (the causal work of a block grows with its index). Blocks are dispatched to the
 // 8 XCDs round-robin (block i to XCD i % 8), and each XCD has its own L2. When the B * KVH head groups
@@ -805,8 +820,8 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(
         dma_rows<HD, BM, 1>(Q + qo, lq.st, q0, T, qs + wu * QT, 0, dfo);
         dma_rows<HD, BM, 1>(dO + qo, lq.st, q0, T, os + wu * QT, 0, dfo);
         const uint32_t lo = (uint32_t)min(lane, T - 1 - q0) * 4;  // rows past T repeat row T - 1
-        __builtin_amdgcn_global_load_lds(reinterpret_cast<const char*>(nLvec + ro + q0) + lo, LDS_AS(void, ls + wu * 2 * BM), 4, 0, 0);
-        __builtin_amdgcn_global_load_lds(reinterpret_cast<const char*>(nDvec + ro + q0) + lo, LDS_AS(void, ls + wu * 2 * BM + BM), 4, 0, 0);
+        dma_vec64(nLvec + ro + q0, lo, ls + wu * 2 * BM);
+        dma_vec64(nDvec + ro + q0, lo, ls + wu * 2 * BM + BM);
     };
     constexpr int kDmaOps = 2 * (QT / 8 / 64) + 2;  // vector-memory instructions per issue_it()
     // The first unit's K / V and first tiles; each later unit's are issued before the previous unit's
