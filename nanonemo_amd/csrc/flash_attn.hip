@@ -1336,7 +1336,23 @@ __global__ __launch_bounds__(256, 2) void fa_bwd_dq_kernel(const u16* __restrict
     for (int i = 0; i < 16; ++i) ndv[i] = nd;
     // MASK: the tile crosses the diagonal or T (a separate instantiation, so that unmasked tiles
     // carry no per-element selects).
-    auto tile = [&](auto mask_tag, int k0, const u16* kb, const u16* vb) __attribute__((always_inline)) {
+    // At head_dim 64 the dQ products of a half run after the masked / unmasked branch, in one copy for both
+    // paths: with a copy inside each path, the two paths left dq in different registers and every half paid a
+    // 16-instruction register copy (32 for masked halves) where they joined (dQ 2-7 % faster at configs 2 and 3
+    // and the small shapes, flat at T = 8192, up to 4-5 % slower for B * T = 8192 at T >= 4096; slower at
+    // head_dim 32, which keeps the products inside each path).
+    constexpr bool kJoinDq = HD == 64;
+    auto dq_products = [&](const u16* kb, const u16x8* sf) __attribute__((always_inline)) {
+#pragma unroll
+        for (int c = 0; c < BN / 16; ++c) {
+            const u16* kc = kb + 16 * c * HD;
+#pragma unroll
+            for (int dt = 0; dt < ND; ++dt)
+                dq[dt] = E::mfma(cat4(ld_tr(kc + kcol[dt][0]), ld_tr(kc + kcol[dt][1])), sf[c], dq[dt]);
+        }
+    };
+    // sfo: this half's 16-bit dS^T operands (chunk c: keys 16c + (j/4)*8 + 4hh + j%4), with kJoinDq.
+    auto tile = [&](auto mask_tag, int k0, const u16* kb, const u16* vb, u16x8* sfo) __attribute__((always_inline)) {
         constexpr bool MASK = decltype(mask_tag)::value;
         u16x8 ka[NT][NS], va[NT][NS];
 #pragma unroll
@@ -1372,20 +1388,17 @@ __global__ __launch_bounds__(256, 2) void fa_bwd_dq_kernel(const u16* __restrict
             for (int i = 0; i < 16; ++i) dp[t][i] = fast_exp2(fmaf(s[t][i], sl2, nl2)) * dp[t][i];
         }
 #pragma unroll
-        for (int c = 0; c < BN / 16; ++c) {
-            const u16x8 sf = pack8<DT>(dp[c >> 1], 8 * (c & 1));  // keys 16c + (j/4)*8 + 4hh + j%4
-            const u16* kc = kb + 16 * c * HD;
-#pragma unroll
-            for (int dt = 0; dt < ND; ++dt)
-                dq[dt] = E::mfma(cat4(ld_tr(kc + kcol[dt][0]), ld_tr(kc + kcol[dt][1])), sf, dq[dt]);
-        }
+        for (int c = 0; c < BN / 16; ++c) sfo[c] = pack8<DT>(dp[c >> 1], 8 * (c & 1));  // keys 16c + (j/4)*8 + 4hh + j%4
+        if constexpr (!kJoinDq) dq_products(kb, sfo);
     };
     auto half = [&](int k0, const u16* kb, const u16* vb) __attribute__((always_inline)) {
         if (qw >= T || k0 > qw + 31) return;  // no visible key in this half for this wave
+        u16x8 sf[BN / 16];
         if (k0 + BN - 1 > qw || k0 + BN > T)
-            tile(std::true_type{}, k0, kb, vb);
+            tile(std::true_type{}, k0, kb, vb, sf);
         else
-            tile(std::false_type{}, k0, kb, vb);
+            tile(std::false_type{}, k0, kb, vb, sf);
+        if constexpr (kJoinDq) dq_products(kb, sf);
     };
     auto step = [&](int it, const u16* kb, const u16* vb) __attribute__((always_inline)) {
         half(it * BT, kb, vb);
